@@ -1,0 +1,168 @@
+/*
+ * lithe_amd: C ABI of the MI355X (gfx950) index-resident multi-adapter LoRA path.
+ *
+ * Every entry point takes device pointers and sizes (no framework types),
+ * validates its arguments before touching the GPU, enqueues its kernels on
+ * the given HIP stream (NULL = the null stream) and returns without
+ * synchronising. Return value: LITHE_OK (0) or a negative LITHE_ERR_* code;
+ * lithe_status_string() names it. The library never allocates device memory:
+ * scratch space is a caller-provided workspace.
+ *
+ * Citations name the reference function each entry point replaces
+ * (paths relative to the reference repository root).
+ */
+#ifndef LITHE_AMD_H
+#define LITHE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status codes */
+#define LITHE_OK             0
+#define LITHE_ERR_NULL      -1   /* a required pointer is NULL */
+#define LITHE_ERR_SHAPE     -2   /* a size is negative, zero where it must not be, or inconsistent */
+#define LITHE_ERR_ALIGN     -3   /* d_in or d_out * rank not a multiple of the 64-value block */
+#define LITHE_ERR_DTYPE     -4   /* unsupported dtype / kind code */
+#define LITHE_ERR_RANGE     -5   /* an index value above 511 (host packing) */
+#define LITHE_ERR_WORKSPACE -6   /* workspace NULL or smaller than lithe_lora_workspace_bytes() */
+#define LITHE_ERR_HIP       -7   /* a HIP launch or query failed */
+#define LITHE_ERR_LEVELS    -8   /* num_levels outside [1, 4] */
+
+/* ---------------------------------------------------------------- dtype codes */
+#define LITHE_DT_BF16  1
+#define LITHE_DT_F32   2
+#define LITHE_DT_F16   3
+#define LITHE_DT_I16   4
+#define LITHE_DT_I32   5
+#define LITHE_DT_I64   6
+#define LITHE_DT_U16   7
+
+/* ---------------------------------------------------------------- index sources */
+/* Packed residency stream: uint64 words, index p of a slot at bits [9(p%7), 9(p%7)+9)
+ * of word p/7, p = block * num_levels + level (lithe/kernels/packed.py:1-9, 38-52). */
+#define LITHE_IDX_PACKED9    1
+/* Level-major integer indices (n_slots, num_levels, n_blocks), as idx_A / idx_B of
+ * lithe/kernels/shared.py:203-204 (int32) and lithe/serve.py:58-60 (int16). */
+#define LITHE_IDX_LEVEL_I32  2
+#define LITHE_IDX_LEVEL_I16  3
+/* Block-major int16 indices (n_blocks, num_levels) per slot (lithe/kernels/packed.py:225-238). */
+#define LITHE_IDX_BLOCK_I16  4
+
+typedef struct lithe_index_src {
+    const void *base;       /* device pointer */
+    int32_t kind;           /* LITHE_IDX_* */
+    int32_t num_levels;     /* 1..4 */
+    int64_t slot_stride;    /* elements (uint64 words for PACKED9) from one slot to the next */
+    int64_t level_stride;   /* elements from one level to the next (LEVEL_* kinds only) */
+    int64_t block_off;      /* first block of the factor inside a slot (a_off / b_off of the layout) */
+    int64_t n_slots;        /* number of addressable slots; larger slot ids are rejected in-kernel */
+} lithe_index_src;
+
+/* Value table of one side: value[l][p] is the pool value at level l of a codeword
+ * coordinate whose 9-bit sign mismatch count popcount((k ^ m_t) & 511) is p, i.e.
+ * sigma_l * (9 - 2p) / 3 in the pool's precision (lithe/codebook.py:59-77). */
+typedef struct lithe_lut {
+    int32_t num_levels;     /* 1..4 */
+    float value[4][10];
+} lithe_lut;
+
+/* ---------------------------------------------------------------- misc */
+int32_t lithe_abi_version(void);                 /* 1 */
+const char *lithe_status_string(int32_t code);
+
+/* ---------------------------------------------------------------- pack / unpack */
+/* Host packing of n uint16 indices into ceil(n/7) words; LITHE_ERR_RANGE if any > 511.
+ * Replaces pack_indices, lithe/kernels/packed.py:38-52. */
+int32_t lithe_pack9_host(const uint16_t *idx, int64_t n, uint64_t *words);
+
+/* Device packing. idx_dtype in {U16, I16, I32, I64}. A value outside [0, 511] writes
+ * 1 to *err_flag (device int32, may be NULL) and its field is packed as 0.
+ * Replaces pack_indices for device-resident indices (lithe/kernels/packed.py:38-52). */
+int32_t lithe_pack9(const void *idx, int32_t idx_dtype, int64_t n, uint64_t *words,
+                    int32_t *err_flag, void *stream);
+
+/* Device unpacking of n indices; out_dtype in {I16, I32, I64}.
+ * Replaces unpack_indices, lithe/kernels/packed.py:55-60. */
+int32_t lithe_unpack9(const uint64_t *words, int64_t n, void *out, int32_t out_dtype, void *stream);
+
+/* ---------------------------------------------------------------- bulk decode */
+/* Decode n_blocks 64-value blocks of each selected slot to dense values:
+ *   out[s][blk][t] = sum_l lut_side(blk).value[l][popcount((k_l ^ m_t) & 511)]   (fp32, l in order)
+ * cast once to out_dtype (BF16: round to nearest even, or F32). sides[blk] = 0 picks lut_a,
+ * 1 picks lut_b (sides NULL: all lut_a). slots: device int32 (n_sel,), NULL = slot 0 for n_sel == 1.
+ * out_sel_stride: elements between the outputs of consecutive selected slots.
+ * err_flag (device int32, nullable) gets bit 1 for a slot id outside [0, n_slots) (its output
+ * is zero-filled) and bit 2 for an unpacked index above 511 (decoded as index 0).
+ * Replaces _decode_packed_kernel / decode_packed (lithe/kernels/packed.py:151-177, 205-222),
+ * _decode_int16_kernel / decode_int16 (:179-195, :225-238) and quant.rvq_decode_blocks
+ * (lithe/quant.py:74-81). */
+int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots, int32_t n_sel,
+                     int64_t n_blocks, const int8_t *sides, const lithe_lut *lut_a,
+                     const lithe_lut *lut_b, void *out, int32_t out_dtype,
+                     int64_t out_sel_stride, int32_t *err_flag, void *stream);
+
+/* ---------------------------------------------------------------- per-sample LoRA delta */
+/* Where the factors of the delta come from. */
+#define LITHE_FACTOR_INDEXED 1   /* decoded in-kernel from index sources + value tables */
+#define LITHE_FACTOR_DENSE   2   /* dense A (n, rank, d_in) and B (n, d_out, rank) */
+
+typedef struct lithe_factors {
+    int32_t kind;               /* LITHE_FACTOR_* */
+    int32_t dense_dtype;        /* DENSE: BF16 or F32 */
+    lithe_index_src a_idx;      /* INDEXED: A (rank, d_in) blocks, row-major flattening */
+    lithe_index_src b_idx;      /* INDEXED: B (d_out, rank) blocks, row-major flattening */
+    lithe_lut lut_a, lut_b;     /* INDEXED */
+    const void *dense_a;        /* DENSE: (n_dense, rank, d_in) */
+    const void *dense_b;        /* DENSE: (n_dense, d_out, rank) */
+    int64_t n_dense;            /* DENSE: number of factor pairs */
+} lithe_factors;
+
+/* Per-sample routing: sample b uses route entries slot[b * n_route + j], j < n_route
+ * (-1 = empty entry). Entry j contributes its adapter at rank offset j * rank of the
+ * rank-stacked factors (lithe/serve.py:85-96). weight_sqrt (nullable) multiplies both
+ * decoded factors of the entry; slot_scale[slot] (nullable) multiplies B first
+ * (alpha / r folded into B, lithe/serve.py:69-73). */
+typedef struct lithe_routes {
+    const int32_t *slot;        /* device (n_batch, n_route) */
+    const float *weight_sqrt;   /* device (n_batch, n_route) or NULL */
+    const float *slot_scale;    /* device (n_slots,) or NULL */
+    int32_t n_route;            /* >= 1 */
+} lithe_routes;
+
+/* Bytes of workspace lithe_lora_delta needs for these sizes. The workspace must be
+ * zero-filled once before its first use; every completed call leaves its counter
+ * region zeroed again. Calls that overlap in time must not share a workspace. */
+int64_t lithe_lora_workspace_bytes(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out,
+                                   int32_t rank, int32_t n_route, int32_t x_dtype);
+
+/* y (n_batch, seq, d_out) receives the per-sample LoRA delta of x (n_batch, seq, d_in):
+ *   mid   = round_x( (x A^T) * mid_scale[b] )          fp32 accumulation, A rows stacked per route
+ *   d     = round_y( round_y(mid B^T) * s_b )           s_b = out_scale_vec ? out_scale_vec[b] : out_scale
+ *   y     = accumulate ? round_y(y + d) : d
+ * round_x / round_y round to the activation / output dtype (BF16: nearest even). The rounding
+ * chain is the reference's: y_lo in x.dtype, delta in out_dtype, `delta * scaling`, `out + delta`.
+ * x_dtype in {BF16, F32}; y_dtype in {BF16, F32}. d_in % 64 == 0 and d_out * rank % 64 == 0.
+ * Samples whose route entries are all empty leave y untouched (accumulate) or zero it.
+ * Replaces _shared_decode_A_matmul_kernel + _shared_decode_B_matmul_kernel and the host
+ * wrapper shared_codebook_lora_delta (lithe/kernels/shared.py:36-157, 197-263), the SGMV pair
+ * _lora_shrink_kernel + _lora_expand_kernel (lithe/kernels/sgmv.py:29-100, 112-160), and the
+ * delta of IndexLoRALinear.forward (lithe/kernels/layers.py:120-131), MultiAdapterLinear.forward
+ * (lithe/serve.py:75-97) and LitheLinear.forward (lithe/module.py:145-156). */
+int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
+                         void *y, int32_t y_dtype, int64_t d_out, int32_t accumulate, int32_t rank,
+                         const lithe_factors *factors, const lithe_routes *routes,
+                         const float *mid_scale, float out_scale, const float *out_scale_vec,
+                         void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Reads the in-kernel error word of a workspace (slot id out of range, index > 511) into
+ * *flags on the host; synchronises the stream. 0 = no error since the last clear. */
+int32_t lithe_workspace_errors(const void *workspace, int32_t *flags, int32_t clear, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LITHE_AMD_H */

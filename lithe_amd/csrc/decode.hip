@@ -1,0 +1,232 @@
+// 9-bit pack / unpack and the bulk decode of packed (or unpacked) index streams.
+//
+// Bulk decode is write-bound: one adapter of the 342-linear FLUX layout reads 2.4 MB of
+// packed words and writes 89.7 MB of bf16. Each thread owns one half of a 64-value
+// block: it decodes the 8 distinct values of its half period (the codeword period is
+// 16, see lithe_common.h) once and stores them to the 4 places they occur, so the
+// per-element cost is a quarter of a direct decode.
+#include <stdint.h>
+
+#include "lithe_common.h"
+
+namespace lithe {
+namespace {
+
+constexpr int kThreads = 256;
+
+__global__ void __launch_bounds__(kThreads) unpack9_kernel(const uint64_t *__restrict__ words, int64_t n,
+                                                          void *__restrict__ out, int32_t out_dtype) {
+    const int64_t w = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n_words = (n + 6) / 7;
+    if (w >= n_words) return;
+    const uint64_t word = words[w];
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+        const int64_t p = w * 7 + j;
+        if (p >= n) break;
+        const uint32_t v = (uint32_t)(word >> (9 * j)) & kIndexMask;
+        if (out_dtype == LITHE_DT_I64) static_cast<int64_t *>(out)[p] = v;
+        else if (out_dtype == LITHE_DT_I32) static_cast<int32_t *>(out)[p] = (int32_t)v;
+        else static_cast<int16_t *>(out)[p] = (int16_t)v;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) pack9_kernel(const void *__restrict__ idx, int32_t idx_dtype,
+                                                        int64_t n, uint64_t *__restrict__ words,
+                                                        int32_t *__restrict__ err) {
+    const int64_t w = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t n_words = (n + 6) / 7;
+    if (w >= n_words) return;
+    uint64_t word = 0;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+        const int64_t p = w * 7 + j;
+        if (p >= n) break;
+        int64_t v;
+        if (idx_dtype == LITHE_DT_U16) v = static_cast<const uint16_t *>(idx)[p];
+        else if (idx_dtype == LITHE_DT_I16) v = static_cast<const int16_t *>(idx)[p];
+        else if (idx_dtype == LITHE_DT_I32) v = static_cast<const int32_t *>(idx)[p];
+        else v = static_cast<const int64_t *>(idx)[p];
+        if (v < 0 || v > (int64_t)kIndexMask) {
+            bad = true;
+            v = 0;
+        }
+        word |= (uint64_t)v << (9 * j);
+    }
+    words[w] = word;
+    if (bad && err) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct DecodeArgs {
+    IdxSrc src;
+    Luts luts;
+    const int32_t *slots;
+    const int8_t *sides;
+    void *out;
+    int64_t n_blocks;
+    int64_t out_sel_stride;
+    int32_t *err;
+};
+
+template <typename OutT>
+__global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
+    __shared__ float lut[2 * kMaxLevels * 10];
+    if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
+    __syncthreads();
+
+    const int64_t half = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t block = half >> 1;
+    if (block >= a.n_blocks) return;
+    const int h = (int)(half & 1);
+    const int sel = blockIdx.y;
+    int64_t slot = a.slots ? a.slots[sel] : 0;
+    OutT *out = static_cast<OutT *>(a.out) + (int64_t)sel * a.out_sel_stride + block * kBlock + 8 * h;
+
+    float v[8];
+    if (slot < 0 || slot >= a.src.n_slots) {
+        if (threadIdx.x == 0 && (block & 127) == 0) record_error(a.err, kErrSlot);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    } else {
+        uint32_t k[kMaxLevels];
+        if (!fetch_indices(a.src, slot, block, k)) record_error(a.err, kErrIndex);
+        const int side = a.sides ? (int)a.sides[block] : 0;
+        const float *tab = lut + side * kMaxLevels * 10;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t m = h ? sign_mask(8 + e) : sign_mask(e);
+            v[e] = decode_value(tab, a.src.levels, k, m);
+        }
+    }
+    if constexpr (sizeof(OutT) == 2) {
+        bf16x8 pk;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pk[e] = (__bf16)v[e];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<bf16x8 *>(out + 16 * j) = pk;
+    } else {
+        f32x4 lo = {v[0], v[1], v[2], v[3]};
+        f32x4 hi = {v[4], v[5], v[6], v[7]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            *reinterpret_cast<f32x4 *>(out + 16 * j) = lo;
+            *reinterpret_cast<f32x4 *>(out + 16 * j + 4) = hi;
+        }
+    }
+}
+
+}  // namespace
+
+// True when blocks [block_off, block_off + n_blocks) of every slot lie inside the slot's
+// extent as described by the strides (guards the kernels against out-of-bounds reads).
+bool src_covers(const lithe_index_src &s, int64_t n_blocks) {
+    const int64_t end = s.block_off + n_blocks;
+    switch (s.kind) {
+        case LITHE_IDX_PACKED9: return end * s.num_levels <= s.slot_stride * 7;
+        case LITHE_IDX_LEVEL_I32:
+        case LITHE_IDX_LEVEL_I16:
+            return end <= s.level_stride && (int64_t)s.num_levels * s.level_stride <= s.slot_stride;
+        case LITHE_IDX_BLOCK_I16: return end * s.num_levels <= s.slot_stride;
+        default: return false;
+    }
+}
+
+namespace {
+
+int32_t check_src(const lithe_index_src *s) {
+    if (!s || !s->base) return LITHE_ERR_NULL;
+    if (s->num_levels < 1 || s->num_levels > kMaxLevels) return LITHE_ERR_LEVELS;
+    if (s->kind < LITHE_IDX_PACKED9 || s->kind > LITHE_IDX_BLOCK_I16) return LITHE_ERR_DTYPE;
+    if (s->slot_stride < 0 || s->level_stride < 0 || s->block_off < 0 || s->n_slots < 1)
+        return LITHE_ERR_SHAPE;
+    return LITHE_OK;
+}
+
+}  // namespace
+
+IdxSrc make_src(const lithe_index_src &s) {
+    IdxSrc r;
+    r.base = s.base;
+    r.slot_stride = s.slot_stride;
+    r.level_stride = s.level_stride;
+    r.block_off = s.block_off;
+    r.n_slots = s.n_slots;
+    r.kind = s.kind;
+    r.levels = s.num_levels;
+    return r;
+}
+
+int32_t validate_src(const lithe_index_src *s) { return check_src(s); }
+
+}  // namespace lithe
+
+using namespace lithe;
+
+extern "C" int32_t lithe_unpack9(const uint64_t *words, int64_t n, void *out, int32_t out_dtype, void *stream) {
+    if (n < 0) return LITHE_ERR_SHAPE;
+    if (out_dtype != LITHE_DT_I16 && out_dtype != LITHE_DT_I32 && out_dtype != LITHE_DT_I64)
+        return LITHE_ERR_DTYPE;
+    if (n == 0) return LITHE_OK;
+    if (!words || !out) return LITHE_ERR_NULL;
+    const int64_t n_words = (n + 6) / 7;
+    const int64_t grid = (n_words + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(unpack9_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, words, n,
+                       out, out_dtype);
+    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+extern "C" int32_t lithe_pack9(const void *idx, int32_t idx_dtype, int64_t n, uint64_t *words, int32_t *err_flag,
+                               void *stream) {
+    if (n < 0) return LITHE_ERR_SHAPE;
+    if (idx_dtype != LITHE_DT_U16 && idx_dtype != LITHE_DT_I16 && idx_dtype != LITHE_DT_I32 &&
+        idx_dtype != LITHE_DT_I64)
+        return LITHE_ERR_DTYPE;
+    if (n == 0) return LITHE_OK;
+    if (!idx || !words) return LITHE_ERR_NULL;
+    const int64_t n_words = (n + 6) / 7;
+    const int64_t grid = (n_words + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(pack9_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, idx, idx_dtype,
+                       n, words, err_flag);
+    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+extern "C" int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots, int32_t n_sel, int64_t n_blocks,
+                                const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b, void *out,
+                                int32_t out_dtype, int64_t out_sel_stride, int32_t *err_flag, void *stream) {
+    int32_t rc = check_src(src);
+    if (rc) return rc;
+    if (!src_covers(*src, n_blocks)) return LITHE_ERR_SHAPE;
+    if (!lut_a || !out) return LITHE_ERR_NULL;
+    if (sides && !lut_b) return LITHE_ERR_NULL;
+    if (n_sel < 1 || n_blocks < 0 || n_sel > 65535) return LITHE_ERR_SHAPE;
+    if (!slots && n_sel != 1) return LITHE_ERR_NULL;
+    if (lut_a->num_levels != src->num_levels || (lut_b && lut_b->num_levels != src->num_levels))
+        return LITHE_ERR_LEVELS;
+    if (out_dtype != LITHE_DT_BF16 && out_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
+    if (n_sel > 1 && out_sel_stride < n_blocks * kBlock) return LITHE_ERR_SHAPE;
+    const int esz = out_dtype == LITHE_DT_BF16 ? 2 : 4;
+    if (((uintptr_t)out & 15u) || ((out_sel_stride * esz) & 15)) return LITHE_ERR_ALIGN;
+    if (n_blocks == 0) return LITHE_OK;
+
+    DecodeArgs a;
+    a.src = make_src(*src);
+    for (int s = 0; s < 2; ++s) {
+        const lithe_lut *t = (s == 0 || !lut_b) ? lut_a : lut_b;
+        for (int l = 0; l < kMaxLevels; ++l)
+            for (int p = 0; p < 10; ++p) a.luts.v[s][l][p] = t->value[l][p];
+    }
+    a.slots = slots;
+    a.sides = sides;
+    a.out = out;
+    a.n_blocks = n_blocks;
+    a.out_sel_stride = out_sel_stride;
+    a.err = err_flag;
+    const int64_t halves = n_blocks * 2;
+    dim3 grid((unsigned)((halves + kThreads - 1) / kThreads), (unsigned)n_sel);
+    if (out_dtype == LITHE_DT_BF16)
+        hipLaunchKernelGGL(decode_kernel<__bf16>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(decode_kernel<float>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}

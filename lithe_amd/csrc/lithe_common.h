@@ -1,0 +1,135 @@
+// Device-side building blocks shared by the gfx950 kernels of liblithe_amd.
+//
+// Codeword arithmetic. The codebook of the reference (lithe/codebook.py:1-17, 59-63)
+// is 3 c_k[t] = sum_{q<9} H[t, q] s_k[q] with H[t, q] = (-1)^popcount(t & q) and
+// s_k[q] = +1 iff bit q of k is set. Writing m_t for the 9-bit mask whose bit q is
+// [popcount(t & q) is even], each term is +1 exactly where bit q of k equals bit q
+// of m_t, so 3 c_k[t] = 9 - 2 popcount((k ^ m_t) & 511). Because q < 16, m_t only
+// depends on t mod 16: every codeword (and every decoded 64-value block) repeats
+// with period 16. A pool value is then a 10-entry table lookup per level,
+// value[l][popcount], which the host derives from the pool tensors it is given.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lithe_amd.h"
+
+namespace lithe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 64;
+constexpr int kMaxLevels = 4;
+constexpr uint32_t kIndexMask = 0x1FFu;
+
+// Error bits written to the workspace error word.
+constexpr int32_t kErrSlot = 1;    // slot id outside [0, n_slots)
+constexpr int32_t kErrIndex = 2;   // level-major index outside [0, 511]
+
+// m_t for t in [0, 16): bit q set iff popcount(t & q) is even (q in [0, 9)).
+__host__ __device__ constexpr uint32_t sign_mask(uint32_t t) {
+    uint32_t m = 0;
+    for (uint32_t q = 0; q < 9; ++q) m |= ((__builtin_popcount(t & q) & 1u) ^ 1u) << q;
+    return m;
+}
+
+// Flat, trivially copyable description of an index source (kernel argument).
+struct IdxSrc {
+    const void *base;
+    int64_t slot_stride;
+    int64_t level_stride;
+    int64_t block_off;
+    int64_t n_slots;
+    int32_t kind;
+    int32_t levels;
+};
+
+// Value tables of both sides (kernel argument, staged into LDS by each kernel).
+struct Luts {
+    float v[2][kMaxLevels][10];
+};
+
+// The L indices of block `block` of slot `slot`. Returns false when an index
+// read from an unpacked source is out of range (it is then replaced by 0).
+__device__ __forceinline__ bool fetch_indices(const IdxSrc &s, int64_t slot, int64_t block,
+                                              uint32_t k[kMaxLevels]) {
+    bool ok = true;
+    const int L = s.levels;
+    if (s.kind == LITHE_IDX_PACKED9) {
+        const uint64_t *w = static_cast<const uint64_t *>(s.base) + slot * s.slot_stride;
+        const int64_t p0 = (s.block_off + block) * L;
+        const int64_t w0 = p0 / 7;
+        const int64_t w1 = (p0 + L - 1) / 7;
+        const uint64_t lo = w[w0];
+        const uint64_t hi = (w1 != w0) ? w[w1] : lo;
+#pragma unroll
+        for (int l = 0; l < kMaxLevels; ++l) {
+            if (l < L) {
+                const int64_t p = p0 + l;
+                const uint64_t word = (p / 7 == w0) ? lo : hi;
+                k[l] = (uint32_t)(word >> (9 * (int)(p % 7))) & kIndexMask;
+            } else {
+                k[l] = 0;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int l = 0; l < kMaxLevels; ++l) {
+            int32_t v = 0;
+            if (l < L) {
+                if (s.kind == LITHE_IDX_LEVEL_I32) {
+                    v = static_cast<const int32_t *>(s.base)[slot * s.slot_stride + l * s.level_stride +
+                                                             s.block_off + block];
+                } else if (s.kind == LITHE_IDX_LEVEL_I16) {
+                    v = static_cast<const int16_t *>(s.base)[slot * s.slot_stride + l * s.level_stride +
+                                                             s.block_off + block];
+                } else {  // LITHE_IDX_BLOCK_I16
+                    v = static_cast<const int16_t *>(s.base)[slot * s.slot_stride +
+                                                             (s.block_off + block) * L + l];
+                }
+                if ((uint32_t)v > kIndexMask) {
+                    ok = false;
+                    v = 0;
+                }
+            }
+            k[l] = (uint32_t)v;
+        }
+    }
+    return ok;
+}
+
+// Decoded value at period position t (mask m = sign_mask(t)) from the L indices,
+// summed in level order in fp32: (v0 + v1) + v2 (+ v3).
+__device__ __forceinline__ float decode_value(const float *lut /* [levels][10] in LDS */, int L,
+                                              const uint32_t k[kMaxLevels], uint32_t m) {
+    float v = lut[__builtin_popcount((k[0] ^ m) & kIndexMask)];
+#pragma unroll
+    for (int l = 1; l < kMaxLevels; ++l)
+        if (l < L) v += lut[l * 10 + __builtin_popcount((k[l] ^ m) & kIndexMask)];
+    return v;
+}
+
+// ---------------------------------------------------------------- dtype helpers
+template <typename T> struct DT;
+template <> struct DT<__bf16> {
+    static constexpr int bytes = 2;
+    __device__ static __forceinline__ __bf16 from_f32(float f) { return (__bf16)f; }
+    __device__ static __forceinline__ float to_f32(__bf16 v) { return (float)v; }
+    __device__ static __forceinline__ float round(float f) { return (float)(__bf16)f; }
+};
+template <> struct DT<float> {
+    static constexpr int bytes = 4;
+    __device__ static __forceinline__ float from_f32(float f) { return f; }
+    __device__ static __forceinline__ float to_f32(float v) { return v; }
+    __device__ static __forceinline__ float round(float f) { return f; }
+};
+
+__device__ __forceinline__ void record_error(int32_t *err, int32_t bits) {
+    if (err) __hip_atomic_fetch_or(err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace lithe

@@ -1,0 +1,77 @@
+"""Prepared ``lithe_lora_delta`` calls: every argument fixed once, one C call per launch.
+
+A serving loop that runs the same modules over the same buffers (the 342
+linears of a FLUX step, or one captured HIP graph of them) builds one
+``PreparedDelta`` per module and replays it: no descriptor building, no
+dtype checks and no allocation on the hot path. Calls that run one after
+another on one stream can share a workspace (``shared_workspace``).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _delta, _hip
+
+
+def workspace_bytes(x_shape, d_out: int, rank: int, n_route: int, x_dtype: torch.dtype) -> int:
+    n = _hip.load().lithe_lora_workspace_bytes(x_shape[0], x_shape[1], x_shape[2], d_out, rank, n_route,
+                                               _hip.dtype_code(x_dtype))
+    _hip.check(int(n) if n < 0 else 0, "lithe_lora_workspace_bytes")
+    return int(n)
+
+
+def shared_workspace(device, nbytes: int) -> torch.Tensor:
+    """A zero-filled workspace (the counter region must start at zero; kernels keep it so)."""
+    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+class PreparedDelta:
+    """y <- delta(x) for fixed tensors; see ``lithe_lora_delta`` in include/lithe_amd.h."""
+
+    def __init__(self, x: torch.Tensor, y: torch.Tensor, *, rank: int, factors: _hip.Factors, route: _hip.Routes,
+                 accumulate: bool, workspace: torch.Tensor, out_scale: float = 1.0,
+                 mid_scale: Optional[torch.Tensor] = None, out_scale_vec: Optional[torch.Tensor] = None,
+                 keep: Sequence = ()):
+        _hip.require_gpu(x, y, workspace)
+        if x.dim() != 3 or y.dim() != 3 or not x.is_contiguous() or not y.is_contiguous():
+            raise ValueError("x and y must be contiguous (B, M, D) tensors")
+        need = workspace_bytes(tuple(x.shape), y.shape[2], rank, route.n_route, x.dtype)
+        if workspace.numel() < need:
+            raise ValueError(f"workspace holds {workspace.numel()} bytes, the call needs {need}")
+        self.x, self.y, self.workspace = x, y, workspace
+        self._keep: List = [factors, route, mid_scale, out_scale_vec, *keep]
+        self._lib = _hip.load()
+        n_batch, seq, d_in = x.shape
+        self._args = (
+            _hip.ptr(x), _hip.dtype_code(x.dtype), n_batch, seq, d_in, _hip.ptr(y), _hip.dtype_code(y.dtype),
+            y.shape[2], int(bool(accumulate)), int(rank), ctypes.byref(factors), ctypes.byref(route),
+            _hip.ptr(mid_scale), ctypes.c_float(float(out_scale)), _hip.ptr(out_scale_vec),
+            _hip.ptr(workspace), workspace.numel())
+        self.tokens = n_batch * seq
+        self.d_in, self.d_out = d_in, y.shape[2]
+
+    def algorithmic_bytes(self) -> int:
+        """x read + y read + y write (accumulate mode), the path's compulsory traffic."""
+        e = self.x.element_size()
+        return self.tokens * (self.d_in * e + 2 * self.d_out * self.y.element_size())
+
+    def __call__(self, stream: Optional[ctypes.c_void_p] = None) -> None:
+        rc = self._lib.lithe_lora_delta(*self._args, stream if stream is not None else _hip.stream_of(self.x.device))
+        if rc:
+            _hip.check(rc, "lithe_lora_delta")
+
+
+def prepare_packed(x: torch.Tensor, y: torch.Tensor, bank_words: torch.Tensor, a_off: int, b_off: int,
+                   num_levels: int, pools: Tuple[torch.Tensor, torch.Tensor], slots: torch.Tensor, rank: int,
+                   scaling: float, workspace: torch.Tensor, accumulate: bool = True) -> PreparedDelta:
+    """Prepared index-resident delta of one module read straight from a packed bank."""
+    lut_a = _hip.lut_from_pools(pools[0], x.dtype)
+    lut_b = _hip.lut_from_pools(pools[1], x.dtype)
+    f = _delta.indexed_factors(_delta.packed_source(bank_words, num_levels, a_off),
+                               _delta.packed_source(bank_words, num_levels, b_off), lut_a, lut_b)
+    sl = slots.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
+    return PreparedDelta(x, y, rank=rank, factors=f, route=_delta.routes(sl), accumulate=accumulate,
+                         workspace=workspace, out_scale=scaling, keep=(sl, bank_words))

@@ -1,0 +1,129 @@
+"""GPU parity of the 9-bit unpack / pack and the bulk decode against the oracle (bit-exact)."""
+import numpy as np
+import pytest
+import torch
+
+import lithe_amd
+from lithe_amd import quant
+from lithe_amd.kernels import (PackedBank, decode_int16, decode_packed, decode_packed_slots, flat_indices,
+                               pack_adapter, pack_indices, split_decoded, unpack_indices)
+from oracle import codebook as ocb
+from oracle import decode as odec
+from oracle import native
+from oracle import packing as opk
+
+from helpers import SMALL, flux_modules, random_adapter
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n", [1, 6, 7, 8, 700, 1001, 2_101_248])
+def test_unpack_bit_exact(n):
+    v = np.random.default_rng(n).integers(0, 512, n)
+    words = opk.pack(v)
+    w = torch.from_numpy(words.view(np.int64)).cuda()
+    got = unpack_indices(w, n).cpu().numpy()
+    assert np.array_equal(got, v)
+    for dt in (torch.int32, torch.int16):
+        assert np.array_equal(unpack_indices(w, n, dtype=dt).cpu().numpy().astype(np.int64), v)
+
+
+def test_device_pack_matches_oracle_and_rejects_512():
+    v = np.random.default_rng(3).integers(0, 512, 12345)
+    for dt in (torch.int16, torch.int32, torch.int64):
+        got = pack_indices(torch.from_numpy(v).to(dt).cuda())
+        assert np.array_equal(got.view(torch.int64).cpu().numpy().view(np.uint64), opk.pack(v))
+    with pytest.raises(ValueError):
+        pack_indices(torch.tensor([3, 512, 1], device="cuda"))
+    with pytest.raises(ValueError):
+        pack_indices(torch.tensor([-1], device="cuda"))
+
+
+def _oracle_decode_bits(ad):
+    words, lay = opk.pack_adapter(ad)
+    pa, pb = ocb.twin_pools()
+    f32 = odec.decode_packed(words, lay, pa, pb)
+    return f32, odec.bf16_bits(f32), lay
+
+
+@pytest.mark.parametrize("mods,rank,seed", [(SMALL, 16, 4), (SMALL + [("wide", 3072, 9216)], 16, 4),
+                                            (SMALL, 8, 3), (SMALL, 4, 1)])
+def test_decode_packed_bit_exact(mods, rank, seed):
+    ad = random_adapter(mods, rank=rank, seed=seed)
+    f32, bits, _ = _oracle_decode_bits(ad)
+    words, layout = pack_adapter(ad)
+    pa, pb = (p.cuda() for p in lithe_amd.twin_pools())
+    w = words.cuda()
+    out = decode_packed(w, layout, pa, pb)
+    assert out.dtype == torch.bfloat16 and out.shape == (layout.total_blocks, 64)
+    assert np.array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), bits)
+    out32 = decode_packed(w, layout, pa, pb, dtype=torch.float32)
+    assert np.array_equal(out32.cpu().numpy().view(np.uint32), f32.view(np.uint32))
+    # int16 block-major source decodes identically (the reference's residency A/B check)
+    idx16 = torch.from_numpy(flat_indices(ad, layout).astype(np.int16)).view(-1, layout.num_levels).cuda()
+    assert torch.equal(decode_int16(idx16, layout, pa, pb), out)
+    # per-module views equal quant.decode -> bf16 (tests/test_kernels.py:166-179 of the reference)
+    got = split_decoded(out, layout)
+    pa_np, pb_np = ocb.twin_pools()
+    for m in ad.modules:
+        a = odec.decode(ad.indices[m["name"]]["A"], m["shape_a"], pa_np)
+        b = odec.decode(ad.indices[m["name"]]["B"], m["shape_b"], pb_np)
+        assert np.array_equal(got[m["name"]][0].view(torch.int16).cpu().numpy().view(np.uint16), odec.bf16_bits(a))
+        assert np.array_equal(got[m["name"]][1].view(torch.int16).cpu().numpy().view(np.uint16), odec.bf16_bits(b))
+
+
+def test_decode_full_flux_layout_matches_c_oracle():
+    """All 342 FLUX linears of one rank-16 adapter (700,416 blocks), against the C restatement."""
+    ad = random_adapter(flux_modules(), rank=16, seed=11)
+    words, layout = pack_adapter(ad)
+    assert layout.total_blocks == 700_416 and layout.num_words == 300_179
+    pa, pb = ocb.twin_pools()
+    ref_bits = native.decode(words.view(torch.int64).numpy().view(np.uint64), layout.total_blocks, 3,
+                             layout.sides.numpy(), pa, pb, want="bf16")
+    out = decode_packed(words.cuda(), layout, *(p.cuda() for p in lithe_amd.twin_pools()))
+    assert np.array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), ref_bits)
+
+
+def test_quant_decode_fp32_exact_and_levels():
+    rng = np.random.default_rng(7)
+    for L in (1, 2, 3, 4):
+        scales = [0.06, 0.03, 0.01, 0.005][:L]
+        pools = ocb.pools(scales)
+        idx = rng.integers(0, 512, (L, 777))
+        want = odec.rvq_decode(idx, pools)
+        got = quant.rvq_decode_blocks(torch.from_numpy(idx).cuda(), torch.from_numpy(pools).cuda())
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32)), L
+        # 7 x 7103 = 49,721 values: 777 blocks, the last one zero-padded
+        w = quant.decode(torch.from_numpy(idx).cuda(), (7, 7103), torch.from_numpy(pools).cuda())
+        assert w.shape == (7, 7103)
+        assert np.array_equal(w.cpu().numpy().view(np.uint32),
+                              odec.decode(idx, (7, 7103), pools).view(np.uint32))
+
+
+def test_bank_multi_slot_decode():
+    ads = [random_adapter(SMALL, rank=16, seed=s) for s in range(5)]
+    bank, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bank.add(w)
+    slots = torch.tensor([4, 0, 2, 2], dtype=torch.int32, device="cuda")
+    out = bank.decode_slots(slots)
+    for i, s in enumerate([4, 0, 2, 2]):
+        _, bits, _ = _oracle_decode_bits(ads[s])
+        assert np.array_equal(out[i].view(torch.int16).cpu().numpy().view(np.uint16), bits)
+    dec = bank.decode(1)
+    want = split_decoded(decode_packed(words[1].cuda(), bank.layout, bank.pool_a, bank.pool_b), bank.layout)
+    for name in want:
+        assert torch.equal(dec[name][0], want[name][0]) and torch.equal(dec[name][1], want[name][1])
+
+
+def test_bank_random_fill_fields_in_range():
+    ad = random_adapter(SMALL, rank=16, seed=1)
+    bank, words = PackedBank.from_adapters([ad], "cuda")
+    bank.add(words[0])
+    bank.fill_random(7, generator=torch.Generator(device="cuda").manual_seed(0))
+    assert bank.num_slots == 7
+    w = bank.words.cpu().numpy().view(np.uint64)
+    assert (w >> np.uint64(63) == 0).all()
+    n = bank.layout.num_indices
+    fields = opk.unpack(w[3], bank.layout.num_words * 7)
+    assert (fields[n:] == 0).all() and fields[:n].max() <= 511
