@@ -1,0 +1,331 @@
+#!/usr/bin/env python
+"""Benchmark of the index-resident multi-adapter LoRA delta on one MI355X.
+
+Default workload (one "step" = one sweep of all 342 FLUX.1-dev target linears at
+1024^2): B = 14 samples x 4,608 tokens (4,096 image + 512 text), bf16, rank 16,
+every sample routed to a distinct adapter of a 10,000-adapter bank held as
+bit-packed 9-bit indices (24.0 GB resident). Each module adds its delta into a
+precomputed base output: y += (x A_j^T) B_j^T with A_j, B_j decoded on the fly
+inside the kernels. Inputs are synthetic (x, y ~ N(0, 1); uniformly random
+9-bit fields) and already resident in HBM; x / y buffers rotate so the 256 MB
+Infinity Cache cannot serve a module from a previous module's data.
+
+    python bench.py [--steps K] [--warmup W] [--config flux342|ffn|hb|decode]
+
+Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
+``roofline`` covers the per-module delta call (shrink + expand kernels) against
+the HBM roofline with the algorithmic bytes 2 d_in + 4 d_out per token (x read,
+y read + write) plus the packed index words of the routed adapters;
+``cpu_baseline`` times the oracle (numpy restatement of the reference's
+PyTorch path) on one sample per module class on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+RANK = 16
+
+
+def flux_modules(img_tokens: int, txt_tokens: int):
+    """(name, d_in, d_out, tokens per sample) of the 342 FLUX.1-dev target linears, model order."""
+    mods = []
+    for i in range(19):
+        p = f"transformer_blocks.{i}."
+        for n in ("attn.to_q", "attn.to_k", "attn.to_v", "attn.to_out.0"):
+            mods.append((p + n, 3072, 3072, img_tokens))
+        for n in ("attn.add_q_proj", "attn.add_k_proj", "attn.add_v_proj", "attn.to_add_out"):
+            mods.append((p + n, 3072, 3072, txt_tokens))
+        mods += [(p + "ff.net.0.proj", 3072, 12288, img_tokens), (p + "ff.net.2", 12288, 3072, img_tokens),
+                 (p + "ff_context.net.0.proj", 3072, 12288, txt_tokens),
+                 (p + "ff_context.net.2", 12288, 3072, txt_tokens)]
+    for i in range(38):
+        p = f"single_transformer_blocks.{i}."
+        for n in ("attn.to_q", "attn.to_k", "attn.to_v"):
+            mods.append((p + n, 3072, 3072, img_tokens + txt_tokens))
+    return mods
+
+
+class Workload:
+    """Bank, buffers and prepared per-module calls of one configuration."""
+
+    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0):
+        import numpy as np
+        import torch
+
+        from lithe_amd.kernels import PackedBank, PackedLayout
+        from lithe_amd.kernels.prepared import prepare_packed, shared_workspace, workspace_bytes
+
+        self.name, self.mods, self.batch = name, mods, batch
+        dev = torch.device("cuda:0")
+        layout_mods = layout_mods or mods
+        layout = PackedLayout.from_modules(
+            [{"name": n, "shape_a": [RANK, di], "shape_b": [do, RANK]} for n, di, do, _ in layout_mods],
+            num_levels=3, block_size=64, scaling=1.0)
+        self.bank = PackedBank(layout, dev, capacity=n_slots)
+        self.bank.fill_random(n_slots, generator=torch.Generator(device=dev).manual_seed(seed))
+        self.assign = torch.tensor(assign, dtype=torch.int32, device=dev)
+        pools = (self.bank.pool_a.to(torch.bfloat16), self.bank.pool_b.to(torch.bfloat16))
+
+        # rotating buffers per (feature dim, tokens) class; copies so that the reuse
+        # distance of every buffer exceeds the 256 MB last-level cache
+        gen = torch.Generator(device=dev).manual_seed(seed + 1)
+        self._bufs, self._next = {}, {}
+
+        def buf(d, m):
+            key = (d, m)
+            if key not in self._bufs:
+                nbytes = batch * m * d * 2
+                copies = 2 if nbytes >= (512 << 20) else 4
+                self._bufs[key] = [torch.randn(batch, m, d, device=dev, generator=gen).to(torch.bfloat16)
+                                   for _ in range(copies)]
+                self._next[key] = 0
+            i = self._next[key]
+            self._next[key] = (i + 1) % len(self._bufs[key])
+            return self._bufs[key][i]
+
+        need = max(workspace_bytes((batch, m, di), do, RANK, 1, torch.bfloat16) for _, di, do, m in mods)
+        self.workspace = shared_workspace(dev, need)
+        self.calls = []
+        for n, di, do, m in mods:
+            _, _, _, a_off, b_off = layout.module(n)
+            x, y = buf(di, m), buf(do, m)
+            self.calls.append(prepare_packed(x, y, self.bank.words, a_off, b_off, 3, pools, self.assign, RANK,
+                                             1.0, self.workspace, accumulate=True))
+        self.tokens = batch * max(m for _, _, _, m in mods) if name != "ffn" else batch * mods[0][3]
+        self.index_bytes = len(set(np.asarray(assign).tolist())) * layout.num_words * 8
+        self.alg_bytes = sum(c.algorithmic_bytes() for c in self.calls) + self.index_bytes
+
+    def sweep(self, stream):
+        for c in self.calls:
+            c(stream)
+
+
+def time_sweeps(wl, steps, warmup, use_graph):
+    import ctypes
+
+    import torch
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    for _ in range(warmup):
+        wl.sweep(sp)
+    torch.cuda.synchronize()
+    graph = None
+    if use_graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            wl.sweep(ctypes.c_void_p(side.cuda_stream))
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            wl.sweep(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        for _ in range(max(1, warmup)):
+            graph.replay()
+        torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            wl.sweep(sp)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, graph is not None
+
+
+def per_call_times(wl, sweeps=2):
+    """Mean duration (ms) of every module's delta call, from HIP events on the launch stream."""
+    import ctypes
+
+    import torch
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    n = len(wl.calls)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    tot = [0.0] * n
+    for _ in range(sweeps):
+        ev[0].record(stream)
+        for i, c in enumerate(wl.calls):
+            c(sp)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        for i in range(n):
+            tot[i] += ev[i].elapsed_time(ev[i + 1])
+    return [t / sweeps for t in tot]
+
+
+def copy_bandwidth_gbps():
+    import torch
+    a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(10):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / 10
+    del a, b
+    return 2 * (1 << 30) / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(mods, batch, budget_s=25.0):
+    """Oracle (numpy restatement of the reference's shared-codebook path) on the host cores.
+
+    Sample: one sample (all its tokens) of one module per (d_in, d_out, tokens) class,
+    extrapolated to the whole sweep by class multiplicity and batch size.
+    """
+    import numpy as np
+
+    from oracle import codebook as ocb
+    from oracle import delta as odelta
+    from oracle import packing as opk
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = len(os.sched_getaffinity(0))
+    classes = {}
+    for _, di, do, m in mods:
+        classes[(di, do, m)] = classes.get((di, do, m), 0) + 1
+    pa, pb = ocb.twin_pools()
+    rng = np.random.default_rng(0)
+    total_s, t0 = 0.0, time.perf_counter()
+    timed = 0
+    for (di, do, m), count in sorted(classes.items(), key=lambda kv: kv[0][2]):
+        ia = rng.integers(0, 512, (1, 3, opk.num_blocks((RANK, di))))
+        ib = rng.integers(0, 512, (1, 3, opk.num_blocks((do, RANK))))
+        x = rng.standard_normal((1, m, di)).astype(np.float32)
+        y = rng.standard_normal((1, m, do)).astype(np.float32)
+        t = time.perf_counter()
+        odelta.index_linear(y, odelta.shared_delta(x, ia, pa, ib, pb, [0], RANK, do, 1.0, "bf16"), "bf16")
+        dt = time.perf_counter() - t
+        total_s += dt * count * batch
+        timed += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    tokens = batch * max(m for _, _, _, m in mods)
+    return {"value": tokens / total_s if timed == len(classes) else None, "unit": "tokens/s",
+            "cores": threads, "kind": "port",
+            "sample": f"oracle shared_delta + index_linear, 1 sample x 1 module of each of {len(classes)} "
+                      f"(d_in, d_out, tokens) classes, scaled by class count x batch {batch}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="flux342", choices=["flux342", "ffn", "hb"])
+    ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--slots", type=int, default=None, help="bank size (default: the configuration's)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path needs no "
+              "collective: samples shard across GPUs with no exchange).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from lithe_amd.kernels import _hip
+    _hip.load()
+    rng = np.random.default_rng(1234)
+    if args.config == "flux342":
+        mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
+        assign = rng.choice(n_slots, batch, replace=False)
+        wl = Workload("flux342", mods, batch, n_slots, assign)
+        workload = "FLUX.1-dev 342 linears, 1024^2: B=14 x 4608 tokens (4096 img + 512 txt), 10k-adapter packed bank"
+    elif args.config == "hb":
+        mods, batch, n_slots = flux_modules(256, 512), 96, args.slots or 10_000
+        ranks = np.arange(1, n_slots + 1, dtype=np.float64)
+        p = ranks ** -1.1
+        p /= p.sum()
+        perm = rng.permutation(n_slots)
+        assign = perm[rng.choice(n_slots, batch, p=p)]
+        wl = Workload("hb", mods, batch, n_slots, assign)
+        workload = "FLUX.1-dev 342 linears, 256^2: B=96 x 768 tokens (256 img + 512 txt), Zipf(1.1) over 10k bank"
+    else:
+        full = flux_modules(1024, 512)
+        mods = [("transformer_blocks.0.ff.net.0.proj", 3072, 12288, 1536),
+                ("transformer_blocks.0.ff.net.2", 12288, 3072, 1536)]
+        batch, n_slots = 14, args.slots or 1_000
+        assign = rng.choice(n_slots, batch, replace=False)
+        wl = Workload("ffn", mods, batch, n_slots, assign, layout_mods=full)
+        workload = "FLUX FFN pair 3072->12288->3072 at 512^2: B=14 x 1536 tokens, 1k-adapter packed bank"
+
+    ms, graphed = time_sweeps(wl, args.steps, args.warmup, not args.no_graph)
+    tokens = wl.tokens
+    value = tokens / (ms * 1e-3)
+    per = per_call_times(wl)
+    call_ms = sum(per)
+    achieved = wl.alg_bytes / (call_ms * 1e-3) / 1e9
+    classes = {}
+    for (n, di, do, m), t, c in zip(wl.mods, per, wl.calls):
+        k = f"{di}->{do} x {m}"
+        e = classes.setdefault(k, {"count": 0, "ms": 0.0, "bytes": 0})
+        e["count"] += 1
+        e["ms"] += t
+        e["bytes"] += c.algorithmic_bytes()
+    for e in classes.values():
+        e["GBps"] = round(e["bytes"] / (e["ms"] * 1e-3) / 1e9, 1)
+        e["ms"] = round(e["ms"], 3)
+        del e["bytes"]
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            traffic = json.load(fh).get("hbm_bytes_per_launch")
+    copy_gbps = copy_bandwidth_gbps()
+    cpu = None if args.no_cpu else cpu_baseline(wl.mods, batch)
+    line = {
+        "metric": "adapter-delta tokens/s + achieved HBM GB/s (% peak), FLUX linears, B=14 mixed",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": workload, "modules": len(wl.mods), "global_batch": batch,
+                   "tokens_per_step": tokens, "rank": RANK, "bank_slots": n_slots,
+                   "bank_GB": round(wl.bank.words.numel() * 8 / 1e9, 2), "hip_graph": graphed},
+        "achieved_GBps": round(wl.alg_bytes / (ms * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(wl.alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {"kernel": "lithe_lora_delta (shrink + expand, one call per module)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_step": wl.alg_bytes,
+                     "mean_call_ms": round(call_ms / len(per), 5)},
+        "classes": classes,
+        "copy_GBps": round(copy_gbps, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
