@@ -1,25 +1,29 @@
-// Per-sample LoRA delta with the factors decoded on the fly (or read dense):
+// Per-sample LoRA delta with the factors decoded from index streams (or read dense):
 //
-//   shrink:  mid[row, g*16 + r] = round_x( sum_k x[row, k] * A_g[r, k] * mid_scale[b] )
-//   expand:  y[row, o]          = round_y( y + round_y( round_y( sum_{g,r} mid * B_g[o, r] ) * s_b ) )
+//   decode:  period[b, j, blk, 0..15] = round_x( w * sum_l lut[l][popc((k_l ^ m_t) & 511)] )
+//   shrink:  mid[row, g*16 + r]      = round_x( sum_k x[row, k] * A_g[r, k] * mid_scale[b] )
+//   expand:  y[row, o]               = round_y( y + round_y( round_y( sum_{g,r} mid * B_g[o, r] ) * s_b ) )
+//
+// The codewords repeat with period 16 (lithe_common.h), so a decoded 64-value block is
+// fully described by 16 values. One small decode launch writes those periods for the
+// routed adapters of the batch into the workspace, 4x smaller than the dense factors
+// and far smaller than a tile of x; the shrink and expand kernels then stream x and y
+// and read factor fragments from the cache-resident periods. Nothing is decoded twice.
 //
 // g runs over "rank groups": route entry j of a sample contributes ceil(rank/16) groups of
-// 16 ranks each (rank-stacked mixtures, lithe/serve.py:89-96). Both kernels use gfx950
-// MFMA tiles with 16 tokens per wave:
+// 16 ranks (rank-stacked mixtures, lithe/serve.py:89-96).
 //
-// shrink  v_mfma_f32_16x16x32_bf16 (fp32: 16x16x4 f32). A-operand = decoded factor rows
-//         (lane%16 = rank), B-operand = x^T (lane%16 = token); lane group q = lane/16 owns
-//         k = 8q..8q+7 of each 32-wide step, so a row of x is read 64 contiguous bytes per
-//         instruction. The decoded A chunk lives in LDS as one 16-value period per
-//         (rank, block): the period-16 structure of the codebook makes it 4x smaller than
-//         the dense chunk. Long reductions split over K; the last workgroup of a token tile
-//         to finish (atomic ticket) sums the fp32 partials in chunk order, so the result
-//         does not depend on scheduling.
-// expand  v_mfma_f32_16x16x16_bf16 (fp32: 16x16x4 f32) with the decoded B tile as the
+// shrink  v_mfma_f32_16x16x32_bf16 (fp32: 16x16x4 f32), one wave per 16 tokens x K slice.
+//         A-operand = factor rows (lane%16 = rank), B-operand = x^T (lane%16 = token); lane
+//         group q = lane/16 owns k = 8q..8q+7 of each 32-wide step, so every row of x is read
+//         in 64-byte pieces. Loads are software-pipelined two batches deep with no branch
+//         between a load and its use. Waves that split one token group's K range reduce
+//         their fp32 partials through LDS in a fixed order (deterministic).
+// expand  v_mfma_f32_16x16x16_bf16 (fp32: 16x16x4 f32) with the factor B tile as the
 //         A-operand (lane%16 = output row) and mid^T as the B-operand (lane%16 = token).
 //         Output rows are assigned so that each lane ends with 8 consecutive outputs of its
-//         token: y is read-modified-written 16 bytes per lane, 64 contiguous bytes per row
-//         per instruction, with the reference's rounding chain applied in registers.
+//         token: y is read-modified-written 16 bytes per lane with the reference's rounding
+//         chain applied in registers, the next sub-tile's loads in flight.
 #include <stdint.h>
 #include <stdlib.h>
 
@@ -46,11 +50,14 @@ struct LoraArgs {
     const void *x;
     void *y;
     void *mid;
+    void *pat_a;        // (n_batch * n_route, n_rg * 16, d_in / 64, 16) periods of A, rows padded to 16
+    void *pat_b;        // (n_batch * n_route, d_out * rank / 64, 16) periods of B
     int32_t *err;
     int64_t n_batch, seq, d_in, d_out, rows;
+    int64_t nb_a_route, nb_b_route;   // blocks per route entry in pat_a / pat_b
     int32_t rank, G, n_rg, n_route, MR;
-    int32_t tiles_s, tg, Kc, arow, red_off;
-    int32_t tiles_e, subs_e, BO, brs, vec_y;
+    int32_t tiles_s, ks, Kc, arow, red_off;
+    int32_t tiles_e, subs_e, BO, vec_y;
     int32_t accumulate;
     float out_scale;
     const int32_t *r_slot;
@@ -64,211 +71,220 @@ struct LoraArgs {
     int64_t n_slots;
 };
 
-// Route of sample b: slot and sqrt-weight of every rank group, staged in LDS by the
-// first G threads. Returns (uniformly) whether any group is active.
-__device__ __forceinline__ bool load_route(const LoraArgs &a, int64_t b, int64_t *s_slot, float *s_w,
-                                           int *s_any) {
-    const int tid = threadIdx.x;
-    if (tid == 0) *s_any = 0;
-    if (tid >= a.G && tid < kMaxGroups) {
-        s_slot[tid] = -1;
-        s_w[tid] = 0.0f;
-    }
+// Slot of route entry j of sample b, or -1 (empty entry or out of range; the latter is recorded).
+__device__ __forceinline__ int64_t route_slot(const LoraArgs &a, int64_t b, int j, bool record) {
+    const int32_t s = a.r_slot[b * a.n_route + j];
+    if (s >= 0 && (int64_t)s < a.n_slots) return s;
+    if (record && s != -1) record_error(a.err, kErrSlot);
+    return -1;
+}
+
+// ============================================================================ decode
+// One thread per (route entry, block) of A or B: the 16-value period of the block, with the
+// route's multipliers (sqrt mixture weight; alpha / r for B) applied before the cast to the
+// activation dtype. Empty entries and the padding rows of A (rank not a multiple of 16)
+// are written as zeros.
+template <typename XT>
+__global__ void __launch_bounds__(kThreads) decode_periods_kernel(LoraArgs a, int64_t n_a_items,
+                                                                  int64_t n_items) {
+    __shared__ float lut[2 * kMaxLevels * 10];
+    if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
     __syncthreads();
-    if (tid < a.G) {
-        const int j = tid / a.n_rg;
-        const int32_t s = a.r_slot[b * a.n_route + j];
-        int64_t slot = -1;
-        if (s >= 0 && (int64_t)s < a.n_slots) slot = s;
-        else if (s != -1) record_error(a.err, kErrSlot);
-        s_slot[tid] = slot;
-        s_w[tid] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
-        if (slot >= 0) atomicOr(s_any, 1);
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n_items) return;
+    const bool is_a = i < n_a_items;
+    const int64_t li = is_a ? i : i - n_a_items;
+    const int64_t per = is_a ? a.nb_a_route : a.nb_b_route;
+    const int64_t bj = li / per, blk = li % per;
+    const int64_t b = bj / a.n_route;
+    const int j = (int)(bj % a.n_route);
+    const int64_t slot = route_slot(a, b, j, is_a && blk == 0);
+    float v[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) v[t] = 0.0f;
+    int64_t src_blk = blk;
+    bool live = slot >= 0;
+    if (is_a) {
+        // pat_a rows are padded to 16 per rank group: row = blk / row_blocks
+        const int64_t row_blocks = a.d_in / kBlock;
+        const int64_t r = blk / row_blocks;
+        live = live && r < a.rank;
+        src_blk = r * row_blocks + blk % row_blocks;
     }
-    __syncthreads();
-    return *s_any != 0;
+    if (live) {
+        uint32_t k[kMaxLevels];
+        const IdxSrc &src = is_a ? a.a_src : a.b_src;
+        if (!fetch_indices(src, slot, src_blk, k)) record_error(a.err, kErrIndex);
+        const float *tab = lut + (is_a ? 0 : kMaxLevels * 10);
+        const float w = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
+        const float sc = (!is_a && a.s_scale) ? a.s_scale[slot] : 1.0f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float d = decode_value(tab, src.levels, k, sign_mask(t));
+            v[t] = is_a ? d * w : (d * sc) * w;
+        }
+    }
+    XT *dst = static_cast<XT *>(is_a ? a.pat_a : a.pat_b) + li * 16;
+    if constexpr (sizeof(XT) == 2) {
+        bf16x8 p0, p1;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            p0[t] = (__bf16)v[t];
+            p1[t] = (__bf16)v[8 + t];
+        }
+        reinterpret_cast<bf16x8 *>(dst)[0] = p0;
+        reinterpret_cast<bf16x8 *>(dst)[1] = p1;
+    } else {
+#pragma unroll
+        for (int t = 0; t < 16; t += 4) *reinterpret_cast<f32x4 *>(dst + t) = f32x4{v[t], v[t + 1], v[t + 2], v[t + 3]};
+    }
 }
 
 // ============================================================================ shrink
-// Workgroup = 4 waves over a tile of 16*TG tokens; the KS = 4/TG waves that share a
-// 16-token group split the K range and reduce their fp32 partials through LDS in a
-// fixed order (deterministic, no global synchronisation). The decoded A factor is
-// staged through LDS in chunks of Kc; each chunk holds one 16-value period per
-// (rank, block) for decoded factors, or the dense rows for dense factors.
-template <typename XT, int SRC, int GM>
+// Workgroup = 4 waves of one sample; each wave owns 16 tokens and 1/ks of every K chunk
+// (ks waves share a token group). The sample's decoded A periods of a K chunk are copied
+// into LDS once per workgroup, so A fragments come from LDS (ds_read) while x streams
+// through the vector memory path. Waves that split a token group's K range reduce their
+// fp32 partials through LDS in a fixed order (deterministic).
+template <typename XT, int SRC, int GM, int U>
 __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ float lut[kMaxLevels * 10];
-    __shared__ int64_t s_slot[kMaxGroups];
-    __shared__ float s_w[kMaxGroups];
-    __shared__ int s_any;
-
     constexpr bool kBf16 = sizeof(XT) == 2;
-    constexpr int KSTEP = kBf16 ? 32 : 16;        // k covered by one lane-group load of 16 bytes x 4 groups
+    constexpr int KSTEP = kBf16 ? 32 : 16;
+    constexpr int EV = 16 / sizeof(XT);      // elements per 16-byte vector
+    typedef typename std::conditional<kBf16, bf16x8, f32x4>::type XV;
+
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay uniform (SGPR) branches
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
-    const int TG = a.tg, KS = kWaves / a.tg;
-    const int tgi = wave % TG, ksi = wave / TG;
+    const int ks = a.ks, tgw = kWaves / a.ks;
+    const int tgi = wave % tgw, ksi = wave / tgw;
     const int tile = blockIdx.x;
     const int64_t b = tile / a.tiles_s;
     const int mt = tile % a.tiles_s;
-    const int64_t m = (int64_t)mt * 16 * TG + tgi * 16 + r16;
+    const int64_t m = ((int64_t)mt * tgw + tgi) * 16 + r16;
     const bool valid = m < a.seq;
     const int64_t row = b * a.seq + (valid ? m : a.seq - 1);
 
-    if (!load_route(a, b, s_slot, s_w, &s_any)) return;
-    if constexpr (SRC == SRC_INDEXED) {
-        if (tid < kMaxLevels * 10) lut[tid] = (&a.luts.v[0][0][0])[tid];
-    }
+    int64_t gslot[GM];
+#pragma unroll
+    for (int g = 0; g < GM; ++g) gslot[g] = g < a.G ? route_slot(a, b, (g < a.G ? g : 0) / a.n_rg, false) : -1;
 
     XT *chunk = reinterpret_cast<XT *>(smem);
+    float *red = reinterpret_cast<float *>(smem + a.red_off);
+    const int64_t row_blocks = a.d_in / kBlock;
     f32x4 acc[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int64_t row_blocks = a.d_in / kBlock;
-    const XT *xrow = static_cast<const XT *>(a.x) + row * a.d_in;
+    const XT *xrow = static_cast<const XT *>(a.x) + row * a.d_in + (kBf16 ? 8 : 4) * gq;
+    const XT *dummy = static_cast<const XT *>(a.x);
+
     for (int64_t k0 = 0; k0 < a.d_in; k0 += a.Kc) {
         const int kn = (int)std::min<int64_t>(a.Kc, a.d_in - k0);
-        __syncthreads();   // LDS free (previous chunk consumed; lut visible)
+        const int nbk = kn / kBlock;
+        __syncthreads();   // previous chunk consumed
+        // ---- fill: rows (g, r) of the chunk, 16 B per thread per step
         if constexpr (SRC == SRC_INDEXED) {
-            const int L = a.a_src.levels;
-            const int nbk = kn / kBlock;
-            const int items = GM * 16 * nbk;
+            const int per_row = nbk * 16 / EV;
+            const int items = GM * 16 * per_row;
             for (int it = tid; it < items; it += kThreads) {
-                const int cb = it % nbk;
-                const int gr = it / nbk;
+                const int c = it % per_row, gr = it / per_row;
                 const int g = gr >> 4, r = gr & 15;
-                const int rr = (g % a.n_rg) * 16 + r;
-                float v[16];
-                const int64_t slot = s_slot[g];
-                if (slot < 0 || rr >= a.rank) {
-#pragma unroll
-                    for (int t = 0; t < 16; ++t) v[t] = 0.0f;
-                } else {
-                    uint32_t k[kMaxLevels];
-                    const int64_t blk = rr * row_blocks + k0 / kBlock + cb;
-                    if (!fetch_indices(a.a_src, slot, blk, k)) record_error(a.err, kErrIndex);
-                    const float w = s_w[g];
-#pragma unroll
-                    for (int t = 0; t < 16; ++t) v[t] = decode_value(lut, L, k, sign_mask(t)) * w;
-                }
-                XT *dst = chunk + gr * a.arow + cb * 16;
-                if constexpr (kBf16) {
-                    bf16x8 p0, p1;
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        p0[t] = (__bf16)v[t];
-                        p1[t] = (__bf16)v[8 + t];
-                    }
-                    reinterpret_cast<bf16x8 *>(dst)[0] = p0;
-                    reinterpret_cast<bf16x8 *>(dst)[1] = p1;
-                } else {
-#pragma unroll
-                    for (int t = 0; t < 16; t += 4)
-                        *reinterpret_cast<f32x4 *>(dst + t) = f32x4{v[t], v[t + 1], v[t + 2], v[t + 3]};
-                }
+                const int gg = g < a.G ? g : 0;
+                const int j = gg / a.n_rg, rr = (gg % a.n_rg) * 16 + r;
+                f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (g < a.G)
+                    v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.pat_a) +
+                                                         (((b * a.n_route + j) * a.n_rg * 16 + rr) * row_blocks +
+                                                          k0 / kBlock) * 16 + c * EV);
+                *reinterpret_cast<f32x4 *>(chunk + gr * a.arow + c * EV) = v;
             }
         } else {
-            constexpr int EV = 16 / sizeof(XT);     // elements per 16-byte vector
             const int per_row = kn / EV;
             const int items = GM * 16 * per_row;
             for (int it = tid; it < items; it += kThreads) {
-                const int c = it % per_row;
-                const int gr = it / per_row;
+                const int c = it % per_row, gr = it / per_row;
                 const int g = gr >> 4, r = gr & 15;
-                const int rr = (g % a.n_rg) * 16 + r;
-                const int64_t slot = s_slot[g];
+                const int rr = ((g < a.G ? g : 0) % a.n_rg) * 16 + r;
                 f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (slot >= 0 && rr < a.rank)
+                if (g < a.G && gslot[g] >= 0 && rr < a.rank)
                     v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_a) +
-                                                         (slot * a.rank + rr) * a.d_in + k0 + c * EV);
+                                                         (gslot[g] * a.rank + rr) * a.d_in + k0 + c * EV);
                 *reinterpret_cast<f32x4 *>(chunk + gr * a.arow + c * EV) = v;
             }
         }
         __syncthreads();
 
-        // this wave's share of the chunk's k-steps
+        // ---- stream this wave's share of the chunk's k-steps
         const int steps = kn / KSTEP;
-        const int s_lo = ksi * steps / KS, s_hi = (ksi + 1) * steps / KS;
-        const XT *xl = xrow + k0 + (kBf16 ? 8 : 4) * gq;
-        // A-fragment: rank row r16 of group g; position of k-step s inside the chunk
-        auto a_off = [&](int s) -> int {
+        const int s_lo = ksi * steps / ks, s_hi = (ksi + 1) * steps / ks;
+        const XT *xl = xrow + k0;
+        auto a_ptr = [&](int g, int s) -> const XT * {
             if constexpr (SRC == SRC_INDEXED) {
-                return kBf16 ? (s >> 1) * 16 + 8 * (gq & 1) : (s >> 2) * 16 + 4 * gq;
+                return chunk + (g * 16 + r16) * a.arow +
+                       (kBf16 ? (s >> 1) * 16 + 8 * (gq & 1) : (s >> 2) * 16 + 4 * gq);
             } else {
-                return s * KSTEP + (kBf16 ? 8 : 4) * gq;
+                return chunk + (g * 16 + r16) * a.arow + s * KSTEP + (kBf16 ? 8 : 4) * gq;
             }
         };
-        typedef typename std::conditional<kBf16, bf16x8, f32x4>::type XV;
-        constexpr int U = 8;
-        // One batch = U k-steps. A fragments of the batch are read from LDS up front, then
-        // the MFMAs; the next batch's x loads are always in flight (when there is no next
-        // batch every lane reads the same dummy address), so the loop has no branches
-        // between a load and its use.
-        auto compute_batch = [&](const XV *xv, int s0, int nsteps) {
+        struct Batch {
+            XV x[U];
+        };
+        auto load_batch = [&](Batch &bt, int s0, bool real) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                bt.x[u] = *reinterpret_cast<const XV *>(real ? xl + (int64_t)KSTEP * (s0 + u) : dummy);
+        };
+        auto compute_batch = [&](const Batch &bt, int s0, int nsteps) {
             XV av[U][GM];
 #pragma unroll
             for (int u = 0; u < U; ++u)
 #pragma unroll
                 for (int g = 0; g < GM; ++g)
-                    if (u < nsteps)
-                        av[u][g] = *reinterpret_cast<const XV *>(chunk + (g * 16 + r16) * a.arow + a_off(s0 + u));
+                    if (u < nsteps) av[u][g] = *reinterpret_cast<const XV *>(a_ptr(g, s0 + u));
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (u >= nsteps) break;
 #pragma unroll
                 for (int g = 0; g < GM; ++g) {
                     if constexpr (kBf16) {
-                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][g], xv[u], acc[g], 0, 0, 0);
+                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][g], bt.x[u], acc[g], 0, 0, 0);
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][g][e], xv[u][e], acc[g], 0, 0, 0);
+                            acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][g][e], bt.x[u][e], acc[g], 0, 0, 0);
                     }
                 }
             }
         };
-        const XT *dummy = static_cast<const XT *>(a.x);
-        auto load_batch = [&](XV *buf, int s0, bool real) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const XT *ptr = real ? xl + KSTEP * (s0 + u) : dummy;
-                buf[u] = *reinterpret_cast<const XV *>(ptr);
-            }
-        };
         const int nfull = (s_hi - s_lo) / U;
         int s = s_lo;
-        XV xa[U], xb[U];
-        if (nfull > 0) load_batch(xa, s, true);
+        Batch ba, bb;
+        if (nfull > 0) load_batch(ba, s, true);
         for (int i = 0; i < nfull; i += 2) {
-            load_batch(xb, s + U, i + 1 < nfull);
+            load_batch(bb, s + U, i + 1 < nfull);
             __builtin_amdgcn_sched_barrier(0);    // keep the prefetch ahead of this batch's MFMAs
-            compute_batch(xa, s, U);
+            compute_batch(ba, s, U);
             s += U;
             if (i + 1 >= nfull) break;
-            load_batch(xa, s + U, i + 2 < nfull);
+            load_batch(ba, s + U, i + 2 < nfull);
             __builtin_amdgcn_sched_barrier(0);
-            compute_batch(xb, s, U);
+            compute_batch(bb, s, U);
             s += U;
         }
         const int rem = s_hi - s;
         if (rem > 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const XT *ptr = u < rem ? xl + KSTEP * (s + u) : dummy;
-                xa[u] = *reinterpret_cast<const XV *>(ptr);
-            }
-            compute_batch(xa, s, rem);
+            for (int u = 0; u < U; ++u)
+                ba.x[u] = *reinterpret_cast<const XV *>(u < rem ? xl + (int64_t)KSTEP * (s + u) : dummy);
+            compute_batch(ba, s, rem);
         }
     }
 
-    // acc[g][e] = partial sum for token r16, rank 4*gq + e of group g over this wave's k-slices
-    const float ms_b = a.mid_scale ? a.mid_scale[b] : 1.0f;
-    if (KS > 1) {
-        float *red = reinterpret_cast<float *>(smem + a.red_off);
+    // acc[g][e]: token r16, rank 4*gq + e of group g, summed over this wave's k range
+    if (ks > 1) {
 #pragma unroll
         for (int g = 0; g < GM; ++g) *reinterpret_cast<f32x4 *>(red + ((wave * GM + g) * 64 + lane) * 4) = acc[g];
         __syncthreads();
@@ -276,15 +292,16 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
             f32x4 sum = *reinterpret_cast<const f32x4 *>(red + ((tgi * GM + g) * 64 + lane) * 4);
-            for (int k2 = 1; k2 < KS; ++k2)
-                sum += *reinterpret_cast<const f32x4 *>(red + (((k2 * TG + tgi) * GM + g) * 64 + lane) * 4);
+            for (int k2 = 1; k2 < ks; ++k2)
+                sum += *reinterpret_cast<const f32x4 *>(red + (((k2 * tgw + tgi) * GM + g) * 64 + lane) * 4);
             acc[g] = sum;
         }
     }
     if (!valid) return;
+    const float ms_b = a.mid_scale ? a.mid_scale[b] : 1.0f;
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-        if (s_slot[g] < 0) continue;
+        if (g >= a.G || gslot[g] < 0) continue;
         XT *dst = static_cast<XT *>(a.mid) + row * a.MR + g * 16 + 4 * gq;
         if constexpr (kBf16) {
             bf16x4 o;
@@ -299,7 +316,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
 
 // ============================================================================ expand
 template <typename YT>
-__device__ __forceinline__ float finish(float acc, float s, float yold, int accumulate) {
+__device__ __forceinline__ float finish(float acc, float s, float yold, bool accumulate) {
     const float d = DT<YT>::round(DT<YT>::round(acc) * s);
     return accumulate ? DT<YT>::round(yold + d) : d;
 }
@@ -332,14 +349,8 @@ template <> struct Y8<float> {
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC>
 __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    __shared__ float lut[kMaxLevels * 10];
-    __shared__ int64_t s_slot[kMaxGroups];
-    __shared__ float s_w[kMaxGroups];
-    __shared__ int s_any;
-
+    typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
     const int tid = threadIdx.x;
-    // wave index as a scalar: loop bounds derived from it stay uniform (SGPR) branches
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
     const int o_tiles = (int)((a.d_out + a.BO - 1) / a.BO);
@@ -349,88 +360,82 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
     const int mt = tile % a.tiles_e;
     const float s_b = a.out_scale_vec ? a.out_scale_vec[b] : a.out_scale;
 
-    const bool any = load_route(a, b, s_slot, s_w, &s_any);
+    int64_t gslot[GM];
+    bool any = false;
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+        gslot[g] = g < a.G ? route_slot(a, b, g / a.n_rg, false) : -1;
+        any = any || gslot[g] >= 0;
+    }
+    auto sub_row = [&](int sub, bool &valid) -> int64_t {
+        const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + r16;
+        valid = m < a.seq;
+        return b * a.seq + (valid ? m : a.seq - 1);
+    };
     if (!any) {
         if (ACC) return;
         // Empty route in write mode: the delta is zero.
         for (int sub = 0; sub < a.subs_e; ++sub) {
-            const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + r16;
-            if (m >= a.seq) continue;
-            YT *yr = static_cast<YT *>(a.y) + (b * a.seq + m) * a.d_out;
+            bool valid;
+            const int64_t row = sub_row(sub, valid);
+            if (!valid) continue;
+            YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
             for (int o = gq; o < a.BO; o += 4)
                 if (obase + o < a.d_out) yr[obase + o] = DT<YT>::from_f32(0.0f);
         }
         return;
     }
 
-    // ---- B tile (BO outputs x 16 ranks per group) into LDS, in the activation dtype.
-    XT *bt = reinterpret_cast<XT *>(smem);
-    if constexpr (SRC == SRC_INDEXED) {
-        if (tid < kMaxLevels * 10) lut[tid] = (&a.luts.v[1][0][0])[tid];
-        __syncthreads();
-    }
-    {
-        const int L = a.b_src.levels;
-        const int items = GM * a.BO;
-        for (int it = tid; it < items; it += kThreads) {
-            const int g = it / a.BO, ol = it % a.BO;
-            const int64_t o = obase + ol;
-            const int rr0 = (g % a.n_rg) * 16;
-            const int64_t slot = s_slot[g];
-            float v[16];
-            if (slot < 0 || o >= a.d_out) {
-#pragma unroll
-                for (int t = 0; t < 16; ++t) v[t] = 0.0f;
-            } else if constexpr (SRC == SRC_INDEXED) {
-                const float sc = a.s_scale ? a.s_scale[slot] : 1.0f;
-                const float w = s_w[g];
-                int64_t cached = -1;
-                uint32_t k[kMaxLevels] = {0, 0, 0, 0};
-#pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    v[t] = 0.0f;
-                    if (rr0 + t < a.rank) {
-                        const int64_t f = o * a.rank + rr0 + t;
-                        const int64_t blk = f >> 6;
-                        if (blk != cached) {
-                            if (!fetch_indices(a.b_src, slot, blk, k)) record_error(a.err, kErrIndex);
-                            cached = blk;
-                        }
-                        v[t] = (decode_value(lut, L, k, sign_mask((uint32_t)(f & 15))) * sc) * w;
-                    }
-                }
-            } else {
-                const XT *src = static_cast<const XT *>(a.dense_b) + (slot * a.d_out + o) * a.rank;
-#pragma unroll
-                for (int t = 0; t < 16; ++t) v[t] = (rr0 + t < a.rank) ? DT<XT>::to_f32(src[rr0 + t]) : 0.0f;
-            }
-            XT *dst = bt + (g * a.BO + ol) * a.brs;
-#pragma unroll
-            for (int t = 0; t < 16; ++t) dst[t] = DT<XT>::from_f32(v[t]);
-        }
-    }
-    __syncthreads();
-
     // ---- B fragments into registers. MFMA (p, h) row i <-> output 32p + 8(i/4) + 4h + (i%4),
     // so lane (token r16, group gq) ends with outputs 32p + 8gq .. +7 of its token.
     constexpr int NP = BOM / 32;
     const int np = a.BO / 32;
-    typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
     Frag bfr[NP][2][GM];
+    // With rank % 4 == 0 the 4 ranks of a fragment are 4 consecutive values of one period
+    // (f = o * rank + rr is a multiple of 4), so each fragment is one 8-byte (fp32: 16-byte) load.
+    const bool quad = (a.rank & 3) == 0;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int ol = 32 * p + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+            const int64_t o = obase + 32 * p + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
-                if (p < np) {
-                    const XT *src = bt + (g * a.BO + ol) * a.brs + 4 * gq;
-                    if constexpr (sizeof(XT) == 2) bfr[p][h][g] = *reinterpret_cast<const i16x4 *>(src);
-                    else bfr[p][h][g] = *reinterpret_cast<const f32x4 *>(src);
-                } else {
-                    bfr[p][h][g] = Frag{};
+                const int gg = g < a.G ? g : 0;
+                const int j = gg / a.n_rg;
+                const int rr = (gg % a.n_rg) * 16 + 4 * gq;
+                const bool live = p < np && gslot[g] >= 0 && o < a.d_out && rr < a.rank;
+                Frag fr = Frag{};
+                if (live) {
+                    if (SRC == SRC_INDEXED && quad) {
+                        const int64_t f = o * a.rank + rr;
+                        const XT *src = static_cast<const XT *>(a.pat_b) + (b * a.n_route + j) * a.nb_b_route * 16 +
+                                        (f >> 6) * 16 + (f & 15);
+                        if constexpr (sizeof(XT) == 2) fr = *reinterpret_cast<const i16x4 *>(src);
+                        else fr = *reinterpret_cast<const f32x4 *>(src);
+                    } else {
+                        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if (rr + e >= a.rank) break;
+                            if constexpr (SRC == SRC_INDEXED) {
+                                const int64_t f = o * a.rank + rr + e;
+                                v[e] = DT<XT>::to_f32(static_cast<const XT *>(a.pat_b)[
+                                    (b * a.n_route + j) * a.nb_b_route * 16 + (f >> 6) * 16 + (f & 15)]);
+                            } else {
+                                v[e] = DT<XT>::to_f32(static_cast<const XT *>(a.dense_b)[
+                                    (gslot[g] * a.d_out + o) * a.rank + rr + e]);
+                            }
+                        }
+                        if constexpr (sizeof(XT) == 2) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) fr[e] = __builtin_bit_cast(short, (__bf16)v[e]);
+                        } else {
+                            fr = f32x4{v[0], v[1], v[2], v[3]};
+                        }
+                    }
                 }
+                bfr[p][h][g] = fr;
             }
         }
     }
@@ -441,12 +446,14 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
+                // a group without an adapter contributes exact zeros (its mid slot is not written)
+                const Frag m = gslot[g] >= 0 ? mf[g] : Frag{};
                 if constexpr (sizeof(XT) == 2) {
-                    acc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfr[p][h][g], mf[g], acc[h], 0, 0, 0);
+                    acc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfr[p][h][g], m, acc[h], 0, 0, 0);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        acc[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(bfr[p][h][g][e], mf[g][e], acc[h], 0, 0, 0);
+                        acc[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(bfr[p][h][g][e], m[e], acc[h], 0, 0, 0);
                 }
             }
         }
@@ -456,11 +463,11 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
             vals[4 + e] = acc[1][e];
         }
     };
-    // mid fragments; groups without an adapter point at group 0 of the same row (their B
-    // tile is zero), so every lane issues the same unconditional loads.
+    // mid fragments; groups without an adapter read group 0 of the same row (their B
+    // fragments are zero), so every lane issues the same unconditional loads.
     int gsrc[GM];
 #pragma unroll
-    for (int g = 0; g < GM; ++g) gsrc[g] = (g < a.G && s_slot[g] >= 0) ? g : 0;
+    for (int g = 0; g < GM; ++g) gsrc[g] = gslot[g] >= 0 ? g : 0;
     auto load_mid = [&](int64_t row, Frag *mf) {
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
@@ -468,11 +475,6 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
             if constexpr (sizeof(XT) == 2) mf[g] = *reinterpret_cast<const i16x4 *>(src);
             else mf[g] = *reinterpret_cast<const f32x4 *>(src);
         }
-    };
-    auto sub_row = [&](int sub, bool &valid) -> int64_t {
-        const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + r16;
-        valid = m < a.seq;
-        return b * a.seq + (valid ? m : a.seq - 1);
     };
 
     if (a.vec_y) {
@@ -482,6 +484,7 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
         // read one dummy address, so no branch separates a load from its use.
         const int64_t omax = a.d_out - 8;
         const YT *ydummy = static_cast<const YT *>(a.y);
+        const XT *mdummy = static_cast<const XT *>(a.mid);
         struct Sub {
             int64_t row;
             bool valid;
@@ -491,7 +494,12 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
         auto load_sub = [&](Sub &t, int sub, bool real) {
             t.row = sub_row(real ? sub : 0, t.valid);
             t.valid = t.valid && real;
-            load_mid(t.row, t.mf);
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                const XT *src = real ? static_cast<const XT *>(a.mid) + t.row * a.MR + gsrc[g] * 16 + 4 * gq : mdummy;
+                if constexpr (sizeof(XT) == 2) t.mf[g] = *reinterpret_cast<const i16x4 *>(src);
+                else t.mf[g] = *reinterpret_cast<const f32x4 *>(src);
+            }
             if constexpr (ACC) {
 #pragma unroll
                 for (int p = 0; p < NP; ++p)
@@ -560,11 +568,11 @@ int env_int(const char *name, int dflt) {
 
 struct Plan {
     int G, n_rg, GM, MR;
-    int tiles_s, tg, Kc, arow, red_off;
+    int tiles_s, ks, Kc, arow, red_off;
     size_t lds_s;
-    int tiles_e, subs_e, BO, BOM, brs;
-    size_t lds_e;
-    int64_t off_mid, total;
+    int tiles_e, subs_e, BO, BOM, U;
+    int64_t nb_a_route, nb_b_route;
+    int64_t off_mid, off_pa, off_pb, total;
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -577,76 +585,93 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.GM = p.G <= 1 ? 1 : p.G <= 2 ? 2 : p.G <= 4 ? 4 : 8;
     p.MR = p.G * 16;
     const int64_t rows = n_batch * seq;
-    const int target = env_int("LITHE_TARGET_WGS", 1024);
+    const int target = env_int("LITHE_TARGET_WAVES", 2048);
 
-    // shrink: 16*tg tokens per workgroup, the K range split over 4/tg waves per token group.
-    int tg = 4;
-    while (tg > 1 && n_batch * ((seq + 16 * tg - 1) / (16 * tg)) < target) tg /= 2;
-    if (getenv("LITHE_SHRINK_TG")) {
-        const int v = env_int("LITHE_SHRINK_TG", tg);
-        tg = v >= 4 ? 4 : v >= 2 ? 2 : 1;
+    // shrink: one wave per 16 tokens x (K / ks); ks grows until there are enough waves.
+    const int64_t groups = n_batch * ((seq + 15) / 16);
+    int ks = 1;
+    while (ks < 4 && groups * ks < target) ks *= 2;
+    if (getenv("LITHE_SHRINK_KS")) {
+        const int v = env_int("LITHE_SHRINK_KS", ks);
+        ks = v >= 4 ? 4 : v >= 2 ? 2 : 1;
     }
-    p.tg = tg;
-    p.tiles_s = (int)std::max<int64_t>(1, (seq + 16 * tg - 1) / (16 * tg));
+    p.ks = ks;
+    const int tgw = kWaves / ks;
+    p.tiles_s = (int)std::max<int64_t>(1, (seq + 16 * tgw - 1) / (16 * tgw));
+    // LDS chunk of A: GM*16 rows; periods (16 values per 64 k) or dense rows (one value per k)
     const int pad = 16 / xbytes;
     const int budget = env_int("LITHE_CHUNK_LDS", 26 * 1024);
-    const int64_t rowbytes_per_k = dense ? xbytes : 0;      // dense rows: 1 element per k
-    int64_t kc;
-    if (dense) {
-        kc = ((budget / (p.GM * 16 * xbytes) - pad) / 64) * 64;
-    } else {
-        kc = ((budget / (p.GM * 16 * xbytes) - pad) / 16) * 64;    // one 16-value period per 64 k
-    }
-    (void)rowbytes_per_k;
+    int64_t kc = dense ? ((budget / (p.GM * 16 * xbytes) - pad) / 64) * 64
+                       : ((budget / (p.GM * 16 * xbytes) - pad) / 16) * 64;
     kc = std::max<int64_t>(64, kc);
     const int64_t nb_total = d_in / kBlock;
     const int64_t nchunk = (d_in + kc - 1) / kc;
-    const int64_t nb = (nb_total + nchunk - 1) / nchunk;     // balanced chunks
-    p.Kc = (int)(nb * kBlock);
-    p.arow = dense ? (int)(p.Kc + pad) : (int)(nb * 16 + pad);
+    const int64_t nbc = (nb_total + nchunk - 1) / nchunk;     // balanced chunks
+    p.Kc = (int)(nbc * kBlock);
+    p.arow = dense ? (int)(p.Kc + pad) : (int)(nbc * 16 + pad);
     const size_t chunk_bytes = (size_t)p.GM * 16 * p.arow * xbytes;
     p.red_off = (int)((chunk_bytes + 15) & ~size_t(15));
-    p.lds_s = p.red_off + (tg < 4 ? (size_t)kWaves * p.GM * 64 * 16 : 0);
+    p.lds_s = p.red_off + (ks > 1 ? (size_t)kWaves * p.GM * 64 * 16 : 0);
 
     // expand: BO outputs x 64*subs tokens per workgroup.
     int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
     bo_max = std::max(32, bo_max);
+    if (p.GM == 1 && env_int("LITHE_EXPAND_BO", 0) == 128) bo_max = 128;
+    p.U = (p.GM == 1 && env_int("LITHE_SHRINK_U", 4) == 8) ? 8 : 4;
     p.BOM = bo_max;
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);
-    p.brs = 16 + 4;
-    p.lds_e = (size_t)p.GM * p.BO * p.brs * xbytes;
     const int64_t o_tiles = (d_out + p.BO - 1) / p.BO;
-    const int64_t base_items = n_batch * ((seq + 63) / 64) * o_tiles;
-    int subs = (int)std::max<int64_t>(1, std::min<int64_t>(4, base_items / (2 * target)));
+    const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
+    int subs = (int)std::max<int64_t>(1, std::min<int64_t>(4, base_wgs / (2 * target)));
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
 
-    // workspace: [error word | mid]
+    // workspace: [error word | mid | A periods | B periods]
+    p.nb_a_route = (int64_t)p.n_rg * 16 * (d_in / kBlock);
+    p.nb_b_route = (d_out * rank) / kBlock;
     p.off_mid = 256;
-    p.total = align256(p.off_mid + rows * p.MR * xbytes);
+    p.off_pa = align256(p.off_mid + rows * p.MR * xbytes);
+    const int64_t pa_bytes = dense ? 0 : n_batch * n_route * p.nb_a_route * 16 * xbytes;
+    const int64_t pb_bytes = dense ? 0 : n_batch * n_route * p.nb_b_route * 16 * xbytes;
+    p.off_pb = align256(p.off_pa + pa_bytes);
+    p.total = align256(p.off_pb + pb_bytes);
     return p;
 }
 
-template <typename XT, typename YT, int SRC, int GM, int BOM>
+template <typename XT, typename YT, int SRC, int GM, int BOM, int U>
 void launch(const Plan &p, LoraArgs &a, hipStream_t st) {
-    dim3 gs((unsigned)(a.n_batch * p.tiles_s));
-    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM>), gs, dim3(kThreads), p.lds_s, st, a);
+    if constexpr (SRC == SRC_INDEXED) {
+        const int64_t na = a.n_batch * a.n_route * a.nb_a_route;
+        const int64_t nitems = na + a.n_batch * a.n_route * a.nb_b_route;
+        hipLaunchKernelGGL((decode_periods_kernel<XT>), dim3((unsigned)((nitems + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, st, a, na, nitems);
+    }
+    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, U>), dim3((unsigned)(a.n_batch * p.tiles_s)), dim3(kThreads),
+                       p.lds_s, st, a);
     dim3 ge((unsigned)(((a.d_out + p.BO - 1) / p.BO) * a.n_batch * p.tiles_e));
     if (a.accumulate)
-        hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true>), ge, dim3(kThreads), p.lds_e, st, a);
+        hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true>), ge, dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false>), ge, dim3(kThreads), p.lds_e, st, a);
+        hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false>), ge, dim3(kThreads), 0, st, a);
 }
 
 template <typename XT, typename YT, int SRC>
 int32_t dispatch_gm(const Plan &p, LoraArgs &a, hipStream_t st) {
     constexpr bool bf = sizeof(XT) == 2;
     switch (p.GM) {
-        case 1: launch<XT, YT, SRC, 1, bf ? 256 : 128>(p, a, st); break;
-        case 2: launch<XT, YT, SRC, 2, bf ? 256 : 128>(p, a, st); break;
-        case 4: launch<XT, YT, SRC, 4, bf ? 128 : 64>(p, a, st); break;
-        default: launch<XT, YT, SRC, 8, bf ? 64 : 32>(p, a, st); break;
+        case 1:
+            if (p.U == 8) {
+                if (p.BOM == 128) launch<XT, YT, SRC, 1, 128, 8>(p, a, st);
+                else launch<XT, YT, SRC, 1, bf ? 256 : 128, 8>(p, a, st);
+            } else {
+                if (p.BOM == 128) launch<XT, YT, SRC, 1, 128, 4>(p, a, st);
+                else launch<XT, YT, SRC, 1, bf ? 256 : 128, 4>(p, a, st);
+            }
+            break;
+        case 2: launch<XT, YT, SRC, 2, bf ? 256 : 128, 4>(p, a, st); break;
+        case 4: launch<XT, YT, SRC, 4, bf ? 128 : 64, 4>(p, a, st); break;
+        default: launch<XT, YT, SRC, 8, bf ? 64 : 32, 4>(p, a, st); break;
     }
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
 }
@@ -668,10 +693,8 @@ extern "C" int64_t lithe_lora_workspace_bytes(int64_t n_batch, int64_t seq, int6
     if (x_dtype != LITHE_DT_BF16 && x_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
     const int n_rg = (rank + 15) / 16;
     if (n_rg * n_route > kMaxGroups) return LITHE_ERR_SHAPE;
-    // The plan depends on the factor kind only through the LDS capacity; size for the larger.
-    const Plan a = make_plan(n_batch, seq, d_in, d_out, rank, n_route, x_dtype == LITHE_DT_BF16 ? 2 : 4, false);
-    const Plan b = make_plan(n_batch, seq, d_in, d_out, rank, n_route, x_dtype == LITHE_DT_BF16 ? 2 : 4, true);
-    return std::max(a.total, b.total);
+    // The indexed plan needs the period buffers, so it bounds the dense one.
+    return make_plan(n_batch, seq, d_in, d_out, rank, n_route, x_dtype == LITHE_DT_BF16 ? 2 : 4, false).total;
 }
 
 extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
@@ -688,7 +711,8 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     const int n_rg = (rank + 15) / 16;
     if (n_rg * routes->n_route > kMaxGroups) return LITHE_ERR_SHAPE;
     if (n_batch == 0 || seq == 0) return LITHE_OK;
-    if (!x || !y || !routes->slot || !workspace) return workspace ? LITHE_ERR_NULL : LITHE_ERR_WORKSPACE;
+    if (!x || !y || !routes->slot) return LITHE_ERR_NULL;
+    if (!workspace) return LITHE_ERR_WORKSPACE;
     const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
     const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
     if (((uintptr_t)x & 15u) || ((uintptr_t)workspace & 255u)) return LITHE_ERR_ALIGN;
@@ -733,25 +757,28 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     a.y = y;
     a.err = reinterpret_cast<int32_t *>(ws);
     a.mid = ws + p.off_mid;
+    a.pat_a = ws + p.off_pa;
+    a.pat_b = ws + p.off_pb;
     a.n_batch = n_batch;
     a.seq = seq;
     a.d_in = d_in;
     a.d_out = d_out;
     a.rows = n_batch * seq;
+    a.nb_a_route = p.nb_a_route;
+    a.nb_b_route = p.nb_b_route;
     a.rank = rank;
     a.G = p.G;
     a.n_rg = p.n_rg;
     a.n_route = routes->n_route;
     a.MR = p.MR;
     a.tiles_s = p.tiles_s;
-    a.tg = p.tg;
+    a.ks = p.ks;
     a.Kc = p.Kc;
     a.arow = p.arow;
     a.red_off = p.red_off;
     a.tiles_e = p.tiles_e;
     a.subs_e = p.subs_e;
     a.BO = p.BO;
-    a.brs = p.brs;
     a.vec_y = (d_out % 8 == 0) && (((uintptr_t)y & 15u) == 0);
     a.accumulate = accumulate ? 1 : 0;
     a.out_scale = out_scale;
