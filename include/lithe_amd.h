@@ -30,6 +30,7 @@ extern "C" {
 #define LITHE_ERR_WORKSPACE -6   /* workspace NULL or smaller than lithe_lora_workspace_bytes() */
 #define LITHE_ERR_HIP       -7   /* a HIP launch or query failed */
 #define LITHE_ERR_LEVELS    -8   /* num_levels outside [1, 4] */
+#define LITHE_ERR_UNSUPPORTED -9 /* weight_sqrt / slot_scale given with dense factors */
 
 /* ---------------------------------------------------------------- dtype codes */
 #define LITHE_DT_BF16  1
@@ -124,7 +125,8 @@ typedef struct lithe_factors {
  * (-1 = empty entry). Entry j contributes its adapter at rank offset j * rank of the
  * rank-stacked factors (lithe/serve.py:85-96). weight_sqrt (nullable) multiplies both
  * decoded factors of the entry; slot_scale[slot] (nullable) multiplies B first
- * (alpha / r folded into B, lithe/serve.py:69-73). */
+ * (alpha / r folded into B, lithe/serve.py:69-73). Both apply to INDEXED factors only:
+ * with DENSE factors they must be NULL (LITHE_ERR_UNSUPPORTED). */
 typedef struct lithe_routes {
     const int32_t *slot;        /* device (n_batch, n_route) */
     const float *weight_sqrt;   /* device (n_batch, n_route) or NULL */
@@ -132,9 +134,10 @@ typedef struct lithe_routes {
     int32_t n_route;            /* >= 1 */
 } lithe_routes;
 
-/* Bytes of workspace lithe_lora_delta needs for these sizes. The workspace must be
- * zero-filled once before its first use; every completed call leaves its counter
- * region zeroed again. Calls that overlap in time must not share a workspace. */
+/* Bytes of workspace lithe_lora_delta needs for these sizes: a 256-byte head whose first
+ * int32 is the in-kernel error word (zero it before the first use; lithe_workspace_errors
+ * reads and clears it), then the rank-r intermediate x A^T of every token. Calls that
+ * overlap in time must not share a workspace. */
 int64_t lithe_lora_workspace_bytes(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out,
                                    int32_t rank, int32_t n_route, int32_t x_dtype);
 

@@ -53,53 +53,99 @@ struct Luts {
     float v[2][kMaxLevels][10];
 };
 
-// The L indices of block `block` of slot `slot`. Returns false when an index
-// read from an unpacked source is out of range (it is then replaced by 0).
-__device__ __forceinline__ bool fetch_indices(const IdxSrc &s, int64_t slot, int64_t block,
-                                              uint32_t k[kMaxLevels]) {
-    bool ok = true;
+// Raw index data of one block, loaded but not yet decoded: for PACKED9 the two uint64
+// words that hold its L fields (possibly the same word twice), for the unpacked kinds
+// the L integers (levels past L repeat level L - 1).
+struct RawIdx {
+    uint32_t v[4];
+};
+
+// Loads the raw index data of NQ blocks. The kind switch sits outside the block loop and
+// every load is unconditional, so all NQ blocks' loads issue back to back and nothing
+// waits for them until extract_indices() reads the registers.
+template <int NQ>
+__device__ __forceinline__ void load_raw(const IdxSrc &s, const int64_t slot[NQ], const int64_t block[NQ],
+                                         RawIdx r[NQ]) {
+    const int L = s.levels;
+    switch (s.kind) {
+        case LITHE_IDX_PACKED9:
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const uint64_t *w = static_cast<const uint64_t *>(s.base) + slot[q] * s.slot_stride;
+                const int64_t p0 = (s.block_off + block[q]) * L;
+                const uint64_t lo = w[p0 / 7];
+                const uint64_t hi = w[(p0 + L - 1) / 7];
+                r[q].v[0] = (uint32_t)lo;
+                r[q].v[1] = (uint32_t)(lo >> 32);
+                r[q].v[2] = (uint32_t)hi;
+                r[q].v[3] = (uint32_t)(hi >> 32);
+            }
+            break;
+        case LITHE_IDX_LEVEL_I32:
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int l = 0; l < kMaxLevels; ++l)
+                    r[q].v[l] = (uint32_t) static_cast<const int32_t *>(s.base)[
+                        slot[q] * s.slot_stride + (l < L ? l : L - 1) * s.level_stride + s.block_off + block[q]];
+            break;
+        case LITHE_IDX_LEVEL_I16:
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int l = 0; l < kMaxLevels; ++l)
+                    r[q].v[l] = (uint32_t)(int32_t) static_cast<const int16_t *>(s.base)[
+                        slot[q] * s.slot_stride + (l < L ? l : L - 1) * s.level_stride + s.block_off + block[q]];
+            break;
+        default:  // LITHE_IDX_BLOCK_I16
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int l = 0; l < kMaxLevels; ++l)
+                    r[q].v[l] = (uint32_t)(int32_t) static_cast<const int16_t *>(s.base)[
+                        slot[q] * s.slot_stride + (s.block_off + block[q]) * L + (l < L ? l : L - 1)];
+            break;
+    }
+}
+
+// The L indices of block `block` from its raw data. Returns false when an index read from
+// an unpacked source is out of range (it is then replaced by 0).
+__device__ __forceinline__ bool extract_indices(const IdxSrc &s, int64_t block, const RawIdx &r,
+                                                uint32_t k[kMaxLevels]) {
     const int L = s.levels;
     if (s.kind == LITHE_IDX_PACKED9) {
-        const uint64_t *w = static_cast<const uint64_t *>(s.base) + slot * s.slot_stride;
         const int64_t p0 = (s.block_off + block) * L;
         const int64_t w0 = p0 / 7;
-        const int64_t w1 = (p0 + L - 1) / 7;
-        const uint64_t lo = w[w0];
-        const uint64_t hi = (w1 != w0) ? w[w1] : lo;
+        const uint64_t lo = (uint64_t)r.v[0] | ((uint64_t)r.v[1] << 32);
+        const uint64_t hi = (uint64_t)r.v[2] | ((uint64_t)r.v[3] << 32);
 #pragma unroll
         for (int l = 0; l < kMaxLevels; ++l) {
-            if (l < L) {
-                const int64_t p = p0 + l;
-                const uint64_t word = (p / 7 == w0) ? lo : hi;
-                k[l] = (uint32_t)(word >> (9 * (int)(p % 7))) & kIndexMask;
-            } else {
-                k[l] = 0;
-            }
+            const int64_t p = p0 + l;
+            const uint64_t word = (p / 7 == w0) ? lo : hi;
+            k[l] = l < L ? (uint32_t)(word >> (9 * (int)(p % 7))) & kIndexMask : 0u;
         }
-    } else {
+        return true;
+    }
+    bool ok = true;
 #pragma unroll
-        for (int l = 0; l < kMaxLevels; ++l) {
-            int32_t v = 0;
-            if (l < L) {
-                if (s.kind == LITHE_IDX_LEVEL_I32) {
-                    v = static_cast<const int32_t *>(s.base)[slot * s.slot_stride + l * s.level_stride +
-                                                             s.block_off + block];
-                } else if (s.kind == LITHE_IDX_LEVEL_I16) {
-                    v = static_cast<const int16_t *>(s.base)[slot * s.slot_stride + l * s.level_stride +
-                                                             s.block_off + block];
-                } else {  // LITHE_IDX_BLOCK_I16
-                    v = static_cast<const int16_t *>(s.base)[slot * s.slot_stride +
-                                                             (s.block_off + block) * L + l];
-                }
-                if ((uint32_t)v > kIndexMask) {
-                    ok = false;
-                    v = 0;
-                }
-            }
-            k[l] = (uint32_t)v;
+    for (int l = 0; l < kMaxLevels; ++l) {
+        uint32_t v = r.v[l];
+        if (l < L && v > kIndexMask) {   // negative values wrap above 511 as well
+            ok = false;
+            v = 0;
         }
+        k[l] = l < L ? v : 0u;
     }
     return ok;
+}
+
+// The L indices of block `block` of slot `slot` (load_raw + extract_indices for one block).
+__device__ __forceinline__ bool fetch_indices(const IdxSrc &s, int64_t slot, int64_t block,
+                                              uint32_t k[kMaxLevels]) {
+    RawIdx r[1];
+    const int64_t sl[1] = {slot}, bl[1] = {block};
+    load_raw<1>(s, sl, bl, r);
+    return extract_indices(s, block, r[0], k);
 }
 
 // Decoded value at period position t (mask m = sign_mask(t)) from the L indices,

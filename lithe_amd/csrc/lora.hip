@@ -1,14 +1,20 @@
-// Per-sample LoRA delta with the factors decoded from index streams (or read dense):
+// Per-sample LoRA delta with the factors decoded on the fly from index streams (or read dense):
 //
-//   decode:  period[b, j, blk, 0..15] = round_x( w * sum_l lut[l][popc((k_l ^ m_t) & 511)] )
-//   shrink:  mid[row, g*16 + r]      = round_x( sum_k x[row, k] * A_g[r, k] * mid_scale[b] )
-//   expand:  y[row, o]               = round_y( y + round_y( round_y( sum_{g,r} mid * B_g[o, r] ) * s_b ) )
+//   shrink:  mid[row, g*16 + r] = round_x( sum_k x[row, k] * A_g[r, k] * mid_scale[b] )
+//   expand:  y[row, o]          = round_y( y + round_y( round_y( sum_{g,r} mid * B_g[o, r] ) * s_b ) )
+//
+// with A_g / B_g decoded in-kernel: value = round_x( w * sum_l lut[l][popc((k_l ^ m_t) & 511)] )
+// (B: ((d * slot_scale) * w), the reference's fold of alpha / r into B followed by the sqrt
+// mixture weight, lithe/serve.py:69-73, 89-96).
 //
 // The codewords repeat with period 16 (lithe_common.h), so a decoded 64-value block is
-// fully described by 16 values. One small decode launch writes those periods for the
-// routed adapters of the batch into the workspace, 4x smaller than the dense factors
-// and far smaller than a tile of x; the shrink and expand kernels then stream x and y
-// and read factor fragments from the cache-resident periods. Nothing is decoded twice.
+// fully described by 16 values. Each shrink workgroup decodes the periods of its sample's
+// A rows for one K chunk straight from the index stream into LDS (a few KB of index words,
+// cache-resident after the first workgroup of the sample touches them); each expand
+// workgroup decodes the B periods of its output range the same way. Both issue the index
+// loads of a fill together and ahead of the tile's first activation loads (route slots and
+// weights come through scalar loads), so the decode waits for one memory round trip per K
+// chunk while the activation stream is already in flight, and needs no extra launch.
 //
 // g runs over "rank groups": route entry j of a sample contributes ceil(rank/16) groups of
 // 16 ranks (rank-stacked mixtures, lithe/serve.py:89-96).
@@ -17,8 +23,8 @@
 //         A-operand = factor rows (lane%16 = rank), B-operand = x^T (lane%16 = token); lane
 //         group q = lane/16 owns k = 8q..8q+7 of each 32-wide step, so every row of x is read
 //         in 64-byte pieces. Loads are software-pipelined two batches deep with no branch
-//         between a load and its use. Waves that split one token group's K range reduce
-//         their fp32 partials through LDS in a fixed order (deterministic).
+//         between a load and its use. Waves that split one token group's K range reduce their
+//         fp32 partials through LDS in a fixed order (deterministic).
 // expand  v_mfma_f32_16x16x16_bf16 (fp32: 16x16x4 f32) with the factor B tile as the
 //         A-operand (lane%16 = output row) and mid^T as the B-operand (lane%16 = token).
 //         Output rows are assigned so that each lane ends with 8 consecutive outputs of its
@@ -43,6 +49,12 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kMaxGroups = 8;
+// Dynamic LDS head of both kernels: the value table of one side. The tile data (A chunk or
+// B periods) starts at kHead.
+constexpr int kLutFloats = kMaxLevels * 10;
+constexpr int kHead = 256;
+static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
+constexpr int kFillBatch = 2;     // fill items per thread whose loads are issued together
 
 enum { SRC_INDEXED = 1, SRC_DENSE = 2 };
 
@@ -50,14 +62,11 @@ struct LoraArgs {
     const void *x;
     void *y;
     void *mid;
-    void *pat_a;        // (n_batch * n_route, n_rg * 16, d_in / 64, 16) periods of A, rows padded to 16
-    void *pat_b;        // (n_batch * n_route, d_out * rank / 64, 16) periods of B
     int32_t *err;
     int64_t n_batch, seq, d_in, d_out, rows;
-    int64_t nb_a_route, nb_b_route;   // blocks per route entry in pat_a / pat_b
     int32_t rank, G, n_rg, n_route, MR;
-    int32_t tiles_s, ks, Kc, arow, red_off;
-    int32_t tiles_e, subs_e, BO, vec_y;
+    int32_t tiles_s, ks, pb, arow, region, red_off;
+    int32_t tiles_e, subs_e, BO, vec_y, nblk_max;
     int32_t accumulate;
     float out_scale;
     const int32_t *r_slot;
@@ -79,52 +88,18 @@ __device__ __forceinline__ int64_t route_slot(const LoraArgs &a, int64_t b, int 
     return -1;
 }
 
-// ============================================================================ decode
-// One thread per (route entry, block) of A or B: the 16-value period of the block, with the
-// route's multipliers (sqrt mixture weight; alpha / r for B) applied before the cast to the
-// activation dtype. Empty entries and the padding rows of A (rank not a multiple of 16)
-// are written as zeros.
+// m_t of lithe_common.h for a run-time t < 16: bit q of m_t is 1 ^ parity(t & q), and
+// parity(t & q) is linear in the bits of t (bit i of t flips the q that have bit i set).
+__host__ __device__ constexpr uint32_t sign_mask_rt(uint32_t t) {
+    return 0x1FFu ^ (((t & 1u) ? 0xAAu : 0u) ^ ((t & 2u) ? 0xCCu : 0u) ^ ((t & 4u) ? 0xF0u : 0u) ^
+                     ((t & 8u) ? 0x100u : 0u));
+}
+static_assert(sign_mask_rt(0) == sign_mask(0) && sign_mask_rt(5) == sign_mask(5) &&
+                  sign_mask_rt(10) == sign_mask(10) && sign_mask_rt(15) == sign_mask(15),
+              "linear form of the sign masks");
+
 template <typename XT>
-__global__ void __launch_bounds__(kThreads) decode_periods_kernel(LoraArgs a, int64_t n_a_items,
-                                                                  int64_t n_items) {
-    __shared__ float lut[2 * kMaxLevels * 10];
-    if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
-    __syncthreads();
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n_items) return;
-    const bool is_a = i < n_a_items;
-    const int64_t li = is_a ? i : i - n_a_items;
-    const int64_t per = is_a ? a.nb_a_route : a.nb_b_route;
-    const int64_t bj = li / per, blk = li % per;
-    const int64_t b = bj / a.n_route;
-    const int j = (int)(bj % a.n_route);
-    const int64_t slot = route_slot(a, b, j, is_a && blk == 0);
-    float v[16];
-#pragma unroll
-    for (int t = 0; t < 16; ++t) v[t] = 0.0f;
-    int64_t src_blk = blk;
-    bool live = slot >= 0;
-    if (is_a) {
-        // pat_a rows are padded to 16 per rank group: row = blk / row_blocks
-        const int64_t row_blocks = a.d_in / kBlock;
-        const int64_t r = blk / row_blocks;
-        live = live && r < a.rank;
-        src_blk = r * row_blocks + blk % row_blocks;
-    }
-    if (live) {
-        uint32_t k[kMaxLevels];
-        const IdxSrc &src = is_a ? a.a_src : a.b_src;
-        if (!fetch_indices(src, slot, src_blk, k)) record_error(a.err, kErrIndex);
-        const float *tab = lut + (is_a ? 0 : kMaxLevels * 10);
-        const float w = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
-        const float sc = (!is_a && a.s_scale) ? a.s_scale[slot] : 1.0f;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float d = decode_value(tab, src.levels, k, sign_mask(t));
-            v[t] = is_a ? d * w : (d * sc) * w;
-        }
-    }
-    XT *dst = static_cast<XT *>(is_a ? a.pat_a : a.pat_b) + li * 16;
+__device__ __forceinline__ void store16(XT *dst, const float v[16]) {
     if constexpr (sizeof(XT) == 2) {
         bf16x8 p0, p1;
 #pragma unroll
@@ -140,17 +115,30 @@ __global__ void __launch_bounds__(kThreads) decode_periods_kernel(LoraArgs a, in
     }
 }
 
+// One side's value table into LDS. The table sits in the kernel arguments, so lane 0
+// writes it from scalar registers: no vector load, nothing for later loads to wait behind.
+__device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
+    if (tid == 0) {
+#pragma unroll
+        for (int i = 0; i < kLutFloats; ++i) lut[i] = v[i];
+    }
+}
+
 // ============================================================================ shrink
-// Workgroup = 4 waves of one sample; each wave owns 16 tokens and 1/ks of every K chunk
-// (ks waves share a token group). The sample's decoded A periods of a K chunk are copied
-// into LDS once per workgroup, so A fragments come from LDS (ds_read) while x streams
-// through the vector memory path. Waves that split a token group's K range reduce their
-// fp32 partials through LDS in a fixed order (deterministic).
+// Workgroup = 4 waves of one sample; each wave owns 16 tokens and 1/ks of every K piece
+// (ks waves share a token group). K is cut into pieces of pb blocks, and the sample's A
+// rows of a piece are decoded (dense factors: copied) into one of two LDS regions. The
+// piece after next is decoded while the current one streams, so the decode's ALU work
+// runs in the shadow of the activation loads and only piece 0 (and 1) sit in front of
+// the stream. A fragments come from LDS (ds_read) while x streams through the vector
+// memory path. Waves that split a token group's K range reduce their fp32 partials
+// through LDS in a fixed order (deterministic).
 template <typename XT, int SRC, int GM, int U>
 __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     constexpr bool kBf16 = sizeof(XT) == 2;
     constexpr int KSTEP = kBf16 ? 32 : 16;
+    constexpr int SPB = kBlock / KSTEP;      // k-steps per 64-value block
     constexpr int EV = 16 / sizeof(XT);      // elements per 16-byte vector
     typedef typename std::conditional<kBf16, bf16x8, f32x4>::type XV;
 
@@ -167,120 +155,251 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     const bool valid = m < a.seq;
     const int64_t row = b * a.seq + (valid ? m : a.seq - 1);
 
-    int64_t gslot[GM];
-#pragma unroll
-    for (int g = 0; g < GM; ++g) gslot[g] = g < a.G ? route_slot(a, b, (g < a.G ? g : 0) / a.n_rg, false) : -1;
-
-    XT *chunk = reinterpret_cast<XT *>(smem);
+    float *lut = reinterpret_cast<float *>(smem);
+    XT *ring = reinterpret_cast<XT *>(smem + kHead);
     float *red = reinterpret_cast<float *>(smem + a.red_off);
-    const int64_t row_blocks = a.d_in / kBlock;
-    f32x4 acc[GM];
+
+    // Per-group slot and mixture weight. b and g are uniform, so these are scalar loads
+    // (their own counter): nothing below waits behind them.
+    int32_t gs[GM];
+    float gw[GM];
+    bool any = false;
 #pragma unroll
-    for (int g = 0; g < GM; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = 0; g < GM; ++g) {
+        const int j = (g < a.G ? g : 0) / a.n_rg;
+        gs[g] = g < a.G ? (int32_t)route_slot(a, b, j, false) : -1;
+        gw[g] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
+        any = any || gs[g] >= 0;
+    }
+    if (tid < GM && tid < a.G) route_slot(a, b, tid / a.n_rg, true);   // records bad slot ids
+    if (!any) return;    // no adapter on this sample: no mid row is read for it
+    auto group_slot = [&](int g) __attribute__((always_inline)) -> int32_t {    // gs[g] for a run-time g < GM
+        int32_t r = gs[0];
+#pragma unroll
+        for (int q = 1; q < GM; ++q) r = g == q ? gs[q] : r;
+        return r;
+    };
+    auto group_weight = [&](int g) __attribute__((always_inline)) -> float {
+        float r = gw[0];
+#pragma unroll
+        for (int q = 1; q < GM; ++q) r = g == q ? gw[q] : r;
+        return r;
+    };
+    if constexpr (SRC == SRC_INDEXED) stage_lut(lut, a.luts.v[0][0], tid);
+
+    const int nb = (int)(a.d_in / kBlock);
+    const int pb = a.pb;
+    const int npiece = (nb + pb - 1) / pb;
+    auto piece_blocks = [&](int g) __attribute__((always_inline)) { return std::min(pb, nb - g * pb); };
+
+    // ---- fills. Indexed: item = the 16-value period of (row gr, block c) of piece g, at
+    // most kFillBatch items per thread (the plan keeps GM * 16 * pb <= kFillBatch * kThreads);
+    // the index loads of a piece are issued one piece ahead of its decode.
+    auto idx_item = [&](int g, int it, int &gr, int &c, bool &live) __attribute__((always_inline)) -> int64_t {
+        const int nbk = piece_blocks(g);
+        gr = it / nbk;
+        c = it - gr * nbk;
+        const int grp = gr >> 4;
+        const int rr = (grp % a.n_rg) * 16 + (gr & 15);
+        live = group_slot(grp) >= 0 && rr < a.rank;
+        return live ? (int64_t)rr * nb + (int64_t)g * pb + c : 0;
+    };
+    auto idx_load = [&](int g, RawIdx *dst) __attribute__((always_inline)) {
+        if (g >= npiece) return;
+        const int items = GM * 16 * piece_blocks(g);
+        int64_t slot[kFillBatch], blk[kFillBatch];
+#pragma unroll
+        for (int q = 0; q < kFillBatch; ++q) {
+            int gr, c;
+            bool live;
+            blk[q] = idx_item(g, std::min(q * kThreads + tid, items - 1), gr, c, live);
+            slot[q] = live ? group_slot(gr >> 4) : 0;
+        }
+        load_raw<kFillBatch>(a.a_src, slot, blk, dst);
+    };
+    auto idx_store = [&](int g, const RawIdx *src) __attribute__((always_inline)) {
+        if (g >= npiece) return;
+        const int items = GM * 16 * piece_blocks(g);
+        XT *reg = ring + (g & 1) * a.region;
+#pragma unroll
+        for (int q = 0; q < kFillBatch; ++q) {
+            const int it = q * kThreads + tid;
+            if (it >= items) break;
+            int gr, c;
+            bool live;
+            const int64_t blk = idx_item(g, it, gr, c, live);
+            uint32_t k[kMaxLevels];
+            const bool ok = extract_indices(a.a_src, blk, src[q], k);
+            if (live && !ok) record_error(a.err, kErrIndex);
+            const float w = group_weight(gr >> 4);
+            float v[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) v[t] = live ? decode_value(lut, a.a_src.levels, k, sign_mask(t)) * w : 0.0f;
+            store16<XT>(reg + gr * a.arow + c * 16, v);
+            __builtin_amdgcn_sched_barrier(0);    // one item's values live at a time
+        }
+    };
+    // Dense: 16-byte pieces of the factor rows, loaded and stored batch by batch.
+    auto dense_fill = [&](int g) __attribute__((always_inline)) {
+        if (g >= npiece) return;
+        const int per_row = piece_blocks(g) * (kBlock / EV);
+        const int items = GM * 16 * per_row;
+        XT *reg = ring + (g & 1) * a.region;
+        for (int base = 0; base < items; base += kFillBatch * kThreads) {
+            f32x4 v[kFillBatch];
+#pragma unroll
+            for (int q = 0; q < kFillBatch; ++q) {
+                const int it = std::min(base + q * kThreads + tid, items - 1);
+                const int gr = it / per_row, c = it - gr * per_row;
+                const int grp = gr >> 4, rr = (grp % a.n_rg) * 16 + (gr & 15);
+                const bool live = group_slot(grp) >= 0 && rr < a.rank;
+                const int64_t off =
+                    live ? ((int64_t)group_slot(grp) * a.rank + rr) * a.d_in + (int64_t)g * pb * kBlock + c * EV : 0;
+                v[q] = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_a) + off);
+            }
+#pragma unroll
+            for (int q = 0; q < kFillBatch; ++q) {
+                const int it = base + q * kThreads + tid;
+                if (it >= items) break;
+                const int gr = it / per_row, c = it - gr * per_row;
+                const int grp = gr >> 4, rr = (grp % a.n_rg) * 16 + (gr & 15);
+                const bool live = group_slot(grp) >= 0 && rr < a.rank;
+                *reinterpret_cast<f32x4 *>(reg + gr * a.arow + c * EV) = live ? v[q] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    };
+
+    // ---- this wave's k-steps: piece g contributes [g*pb*SPB + lo, g*pb*SPB + hi), cut into
+    // batches of at most U steps that never straddle two pieces.
+    struct Cur {
+        int g, s, hi;
+    };
+    struct Desc {
+        int g, s0, n;
+    };
+    auto share = [&](Cur &c) __attribute__((always_inline)) {
+        const int n = piece_blocks(c.g) * SPB;
+        c.s = c.g * pb * SPB + ksi * n / ks;
+        c.hi = c.g * pb * SPB + (ksi + 1) * n / ks;
+    };
+    auto skip_empty = [&](Cur &c) __attribute__((always_inline)) {
+        while (c.g < npiece && c.s >= c.hi) {
+            ++c.g;
+            if (c.g < npiece) share(c);
+        }
+    };
+    auto next = [&](Cur &c) __attribute__((always_inline)) -> Desc {
+        Desc d{npiece, 0, 0};
+        if (c.g >= npiece) return d;
+        d.g = c.g;
+        d.s0 = c.s;
+        d.n = std::min(U, c.hi - c.s);
+        c.s += d.n;
+        skip_empty(c);
+        return d;
+    };
 
     const XT *xrow = static_cast<const XT *>(a.x) + row * a.d_in + (kBf16 ? 8 : 4) * gq;
     const XT *dummy = static_cast<const XT *>(a.x);
+    struct Batch {
+        XV x[U];
+    };
+    auto load_batch = [&](Batch &bt, const Desc &d) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            bt.x[u] = *reinterpret_cast<const XV *>(u < d.n ? xrow + (int64_t)KSTEP * (d.s0 + u) : dummy);
+    };
+    f32x4 acc[GM];
+#pragma unroll
+    for (int g = 0; g < GM; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute_batch = [&](const Batch &bt, const Desc &d) __attribute__((always_inline)) {
+        const XT *reg = ring + (d.g & 1) * a.region + r16 * a.arow;
+        const int sp = d.s0 - d.g * pb * SPB;    // step inside the piece
+        XV av[U][GM];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                const XT *ap;
+                if constexpr (SRC == SRC_INDEXED)
+                    ap = reg + g * 16 * a.arow + (kBf16 ? ((sp + u) >> 1) * 16 + 8 * (gq & 1) : ((sp + u) >> 2) * 16 + 4 * gq);
+                else
+                    ap = reg + g * 16 * a.arow + (sp + u) * KSTEP + (kBf16 ? 8 : 4) * gq;
+                if (u < d.n) av[u][g] = *reinterpret_cast<const XV *>(ap);
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (u >= d.n) break;
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                if constexpr (kBf16) {
+                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][g], bt.x[u], acc[g], 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][g][e], bt.x[u][e], acc[g], 0, 0, 0);
+                }
+            }
+        }
+    };
 
-    for (int64_t k0 = 0; k0 < a.d_in; k0 += a.Kc) {
-        const int kn = (int)std::min<int64_t>(a.Kc, a.d_in - k0);
-        const int nbk = kn / kBlock;
-        __syncthreads();   // previous chunk consumed
-        // ---- fill: rows (g, r) of the chunk, 16 B per thread per step
+    // ---- prologue: index loads of pieces 0 and 1, then x of the first two batches; the
+    // decode below waits for its own loads only (loads complete in order).
+    RawIdx raw[kFillBatch];
+    {
+        RawIdx raw1[kFillBatch];
         if constexpr (SRC == SRC_INDEXED) {
-            const int per_row = nbk * 16 / EV;
-            const int items = GM * 16 * per_row;
-            for (int it = tid; it < items; it += kThreads) {
-                const int c = it % per_row, gr = it / per_row;
-                const int g = gr >> 4, r = gr & 15;
-                const int gg = g < a.G ? g : 0;
-                const int j = gg / a.n_rg, rr = (gg % a.n_rg) * 16 + r;
-                f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (g < a.G)
-                    v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.pat_a) +
-                                                         (((b * a.n_route + j) * a.n_rg * 16 + rr) * row_blocks +
-                                                          k0 / kBlock) * 16 + c * EV);
-                *reinterpret_cast<f32x4 *>(chunk + gr * a.arow + c * EV) = v;
-            }
+            idx_load(0, raw);
+            idx_load(1, raw1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        Cur cur{0, 0, 0};
+        share(cur);
+        skip_empty(cur);
+        Desc da = next(cur), db = next(cur);
+        Batch ba, bb;
+        load_batch(ba, da);
+        load_batch(bb, db);
+        if constexpr (SRC == SRC_INDEXED) {
+            idx_store(0, raw);
+            idx_store(1, raw1);
+            idx_load(2, raw);
         } else {
-            const int per_row = kn / EV;
-            const int items = GM * 16 * per_row;
-            for (int it = tid; it < items; it += kThreads) {
-                const int c = it % per_row, gr = it / per_row;
-                const int g = gr >> 4, r = gr & 15;
-                const int rr = ((g < a.G ? g : 0) % a.n_rg) * 16 + r;
-                f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                if (g < a.G && gslot[g] >= 0 && rr < a.rank)
-                    v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_a) +
-                                                         (gslot[g] * a.rank + rr) * a.d_in + k0 + c * EV);
-                *reinterpret_cast<f32x4 *>(chunk + gr * a.arow + c * EV) = v;
-            }
+            dense_fill(0);
+            dense_fill(1);
         }
         __syncthreads();
 
-        // ---- stream this wave's share of the chunk's k-steps
-        const int steps = kn / KSTEP;
-        const int s_lo = ksi * steps / ks, s_hi = (ksi + 1) * steps / ks;
-        const XT *xl = xrow + k0;
-        auto a_ptr = [&](int g, int s) -> const XT * {
-            if constexpr (SRC == SRC_INDEXED) {
-                return chunk + (g * 16 + r16) * a.arow +
-                       (kBf16 ? (s >> 1) * 16 + 8 * (gq & 1) : (s >> 2) * 16 + 4 * gq);
-            } else {
-                return chunk + (g * 16 + r16) * a.arow + s * KSTEP + (kBf16 ? 8 : 4) * gq;
-            }
-        };
-        struct Batch {
-            XV x[U];
-        };
-        auto load_batch = [&](Batch &bt, int s0, bool real) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                bt.x[u] = *reinterpret_cast<const XV *>(real ? xl + (int64_t)KSTEP * (s0 + u) : dummy);
-        };
-        auto compute_batch = [&](const Batch &bt, int s0, int nsteps) {
-            XV av[U][GM];
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int g = 0; g < GM; ++g)
-                    if (u < nsteps) av[u][g] = *reinterpret_cast<const XV *>(a_ptr(g, s0 + u));
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (u >= nsteps) break;
-#pragma unroll
-                for (int g = 0; g < GM; ++g) {
-                    if constexpr (kBf16) {
-                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][g], bt.x[u], acc[g], 0, 0, 0);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][g][e], bt.x[u][e], acc[g], 0, 0, 0);
-                    }
+        // ---- main loop. Entering piece g + 1 from g: barrier (all waves are done with piece
+        // g, and piece g + 1 is complete), then piece g + 2 is filled into piece g's region.
+        int pg = 0;
+        auto enter = [&](int g) __attribute__((always_inline)) {
+            while (pg < g) {
+                __syncthreads();
+                if constexpr (SRC == SRC_INDEXED) {
+                    idx_store(pg + 2, raw);
+                    idx_load(pg + 3, raw);
+                } else {
+                    dense_fill(pg + 2);
                 }
+                ++pg;
             }
         };
-        const int nfull = (s_hi - s_lo) / U;
-        int s = s_lo;
-        Batch ba, bb;
-        if (nfull > 0) load_batch(ba, s, true);
-        for (int i = 0; i < nfull; i += 2) {
-            load_batch(bb, s + U, i + 1 < nfull);
-            __builtin_amdgcn_sched_barrier(0);    // keep the prefetch ahead of this batch's MFMAs
-            compute_batch(ba, s, U);
-            s += U;
-            if (i + 1 >= nfull) break;
-            load_batch(ba, s + U, i + 2 < nfull);
+        // batch i sits in ba (i even) or bb (i odd); batch i + 1 is in flight in the other
+        while (da.n > 0) {
+            enter(da.g);
+            compute_batch(ba, da);
+            da = next(cur);
+            load_batch(ba, da);
+            __builtin_amdgcn_sched_barrier(0);    // keep the refill ahead of the next MFMAs
+            if (db.n == 0) break;
+            enter(db.g);
+            compute_batch(bb, db);
+            db = next(cur);
+            load_batch(bb, db);
             __builtin_amdgcn_sched_barrier(0);
-            compute_batch(bb, s, U);
-            s += U;
         }
-        const int rem = s_hi - s;
-        if (rem > 0) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                ba.x[u] = *reinterpret_cast<const XV *>(u < rem ? xl + (int64_t)KSTEP * (s + u) : dummy);
-            compute_batch(ba, s, rem);
-        }
+        enter(npiece - 1);    // every wave passes the same npiece - 1 boundaries
     }
 
     // acc[g][e]: token r16, rank 4*gq + e of group g, summed over this wave's k range
@@ -301,7 +420,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     const float ms_b = a.mid_scale ? a.mid_scale[b] : 1.0f;
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-        if (g >= a.G || gslot[g] < 0) continue;
+        if (gs[g] < 0) continue;
         XT *dst = static_cast<XT *>(a.mid) + row * a.MR + g * 16 + 4 * gq;
         if constexpr (kBf16) {
             bf16x4 o;
@@ -347,8 +466,9 @@ template <> struct Y8<float> {
     }
 };
 
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC>
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
 __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
     typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -367,7 +487,7 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
         gslot[g] = g < a.G ? route_slot(a, b, g / a.n_rg, false) : -1;
         any = any || gslot[g] >= 0;
     }
-    auto sub_row = [&](int sub, bool &valid) -> int64_t {
+    auto sub_row = [&](int sub, bool &valid) __attribute__((always_inline)) -> int64_t {
         const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + r16;
         valid = m < a.seq;
         return b * a.seq + (valid ? m : a.seq - 1);
@@ -386,61 +506,161 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
         return;
     }
 
-    // ---- B fragments into registers. MFMA (p, h) row i <-> output 32p + 8(i/4) + 4h + (i%4),
-    // so lane (token r16, group gq) ends with outputs 32p + 8gq .. +7 of its token.
     constexpr int NP = BOM / 32;
     const int np = a.BO / 32;
-    Frag bfr[NP][2][GM];
-    // With rank % 4 == 0 the 4 ranks of a fragment are 4 consecutive values of one period
-    // (f = o * rank + rr is a multiple of 4), so each fragment is one 8-byte (fp32: 16-byte) load.
-    const bool quad = (a.rank & 3) == 0;
+    // mid fragments; groups without an adapter read group 0 of the same row (their B
+    // fragments are zero), so every lane issues the same unconditional loads.
+    int gsrc[GM];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
+    for (int g = 0; g < GM; ++g) gsrc[g] = gslot[g] >= 0 ? g : 0;
+
+    // Per-route B multipliers (scalar loads: b and the route are uniform). Route j's first
+    // rank group is g = j * n_rg.
+    float gw[GM], gsc[GM];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t o = obase + 32 * p + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+    for (int g = 0; g < GM; ++g) {
+        const int j = (g < a.G ? g : 0) / a.n_rg;
+        gw[g] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
+        gsc[g] = (gslot[g] >= 0 && a.s_scale) ? a.s_scale[gslot[g]] : 1.0f;
+    }
+    auto route_pick = [&](int j, int64_t &slot, float &w, float &sc) __attribute__((always_inline)) {
+        const int g0 = j * a.n_rg;
+        slot = gslot[0];
+        w = gw[0];
+        sc = gsc[0];
 #pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                const int gg = g < a.G ? g : 0;
-                const int j = gg / a.n_rg;
-                const int rr = (gg % a.n_rg) * 16 + 4 * gq;
-                const bool live = p < np && gslot[g] >= 0 && o < a.d_out && rr < a.rank;
-                Frag fr = Frag{};
-                if (live) {
-                    if (SRC == SRC_INDEXED && quad) {
-                        const int64_t f = o * a.rank + rr;
-                        const XT *src = static_cast<const XT *>(a.pat_b) + (b * a.n_route + j) * a.nb_b_route * 16 +
-                                        (f >> 6) * 16 + (f & 15);
-                        if constexpr (sizeof(XT) == 2) fr = *reinterpret_cast<const i16x4 *>(src);
-                        else fr = *reinterpret_cast<const f32x4 *>(src);
-                    } else {
-                        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 1; q < GM; ++q) {
+            slot = g0 == q ? gslot[q] : slot;
+            w = g0 == q ? gw[q] : w;
+            sc = g0 == q ? gsc[q] : sc;
+        }
+    };
+
+    // ---- B tile of this output range into LDS (bp), read from there by every MFMA.
+    // Indexed: the 16-value periods of blocks [blk_lo, blk_lo + nblk) of every route entry,
+    // one item per quarter period (4 values), 2 items per thread per batch.
+    // Dense: rows o in [obase, o_end) of every route entry's B, (route, o - obase, rank).
+    float *lut = reinterpret_cast<float *>(smem);
+    XT *bp = reinterpret_cast<XT *>(smem + kHead);
+    const int64_t blk_lo = (obase * a.rank) >> 6;
+    const int64_t o_end = std::min<int64_t>(obase + a.BO, a.d_out);
+    if constexpr (SRC == SRC_INDEXED) {
+        const int per_route = (int)(((o_end * a.rank + kBlock - 1) >> 6) - blk_lo) * 4;
+        const int items = a.n_route * per_route;
+        RawIdx raw[2];
+        // block of item `it` inside the factor; 0 if its route entry is empty
+        auto dec_block = [&](int it, int64_t &slot, float &w, float &sc) __attribute__((always_inline)) -> int64_t {
+            const int j = it / per_route;
+            route_pick(j, slot, w, sc);
+            const int64_t blk = blk_lo + ((it - j * per_route) >> 2);
+            return slot >= 0 ? blk : 0;
+        };
+        auto dec_load = [&](int base) __attribute__((always_inline)) {
+            int64_t slot[2], blk[2];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (rr + e >= a.rank) break;
-                            if constexpr (SRC == SRC_INDEXED) {
-                                const int64_t f = o * a.rank + rr + e;
-                                v[e] = DT<XT>::to_f32(static_cast<const XT *>(a.pat_b)[
-                                    (b * a.n_route + j) * a.nb_b_route * 16 + (f >> 6) * 16 + (f & 15)]);
-                            } else {
-                                v[e] = DT<XT>::to_f32(static_cast<const XT *>(a.dense_b)[
-                                    (gslot[g] * a.d_out + o) * a.rank + rr + e]);
-                            }
-                        }
-                        if constexpr (sizeof(XT) == 2) {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) fr[e] = __builtin_bit_cast(short, (__bf16)v[e]);
-                        } else {
-                            fr = f32x4{v[0], v[1], v[2], v[3]};
-                        }
-                    }
-                }
-                bfr[p][h][g] = fr;
+            for (int q = 0; q < 2; ++q) {
+                float w, sc;
+                blk[q] = dec_block(std::min(base + q * kThreads + tid, items - 1), slot[q], w, sc);
+                slot[q] = slot[q] >= 0 ? slot[q] : 0;
             }
+            load_raw<2>(a.b_src, slot, blk, raw);
+        };
+        auto dec_store = [&](int base) __attribute__((always_inline)) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int it = base + q * kThreads + tid;
+                if (it >= items) break;
+                const int j = it / per_route;
+                const int rem = it - j * per_route;
+                const int blk = rem >> 2, qt = rem & 3;
+                int64_t slot;
+                float w, sc;
+                uint32_t k[kMaxLevels];
+                const bool ok = extract_indices(a.b_src, dec_block(it, slot, w, sc), raw[q], k);
+                const bool live = slot >= 0;
+                if (live && !ok) record_error(a.err, kErrIndex);
+                XT *dst = bp + ((int64_t)j * a.nblk_max + blk) * 16 + 4 * qt;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[e] = live ? (decode_value(lut, a.b_src.levels, k, sign_mask_rt(4 * qt + e)) * sc) * w : 0.0f;
+                if constexpr (sizeof(XT) == 2) {
+                    bf16x4 pk;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) pk[e] = (__bf16)v[e];
+                    *reinterpret_cast<bf16x4 *>(dst) = pk;
+                } else {
+                    *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+                }
+            }
+        };
+        dec_load(0);
+        stage_lut(lut, a.luts.v[1][0], tid);
+        __syncthreads();
+        dec_store(0);
+        for (int base = 2 * kThreads; base < items; base += 2 * kThreads) {
+            dec_load(base);
+            dec_store(base);
+        }
+    } else {
+        // 16-byte vectors of (o_end - obase) * rank consecutive values per route entry
+        constexpr int EV = 16 / sizeof(XT);
+        const int per_route = (int)((o_end - obase) * a.rank / EV);
+        const int items = a.n_route * per_route;
+        for (int it = tid; it < items; it += kThreads) {
+            const int j = it / per_route, c = it - j * per_route;
+            int64_t slot;
+            float w, sc;
+            route_pick(j, slot, w, sc);
+            f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (slot >= 0)
+                v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_b) +
+                                                     (slot * a.d_out + obase) * a.rank + (int64_t)c * EV);
+            *reinterpret_cast<f32x4 *>(bp + (int64_t)j * a.BO * a.rank + (int64_t)c * EV) = v;
         }
     }
+    __syncthreads();
 
-    auto compute = [&](const Frag *mf, int p, float vals[8]) {
+    // ---- B fragment (p, h, g) from LDS. MFMA (p, h) row i <-> output 32p + 8(i/4) + 4h + (i%4),
+    // so lane (token r16, group gq) ends with outputs 32p + 8gq .. +7 of its token. QUAD
+    // (rank % 4 == 0): the 4 ranks of a fragment are 4 consecutive LDS values, one 8-byte read
+    // (fp32: 16 bytes); dead fragments read a valid address and are zeroed, without branches.
+    auto b_index = [&](int j, int64_t o, int r) __attribute__((always_inline)) -> int64_t {
+        if constexpr (SRC == SRC_INDEXED) {
+            const int64_t f = o * a.rank + r;
+            return ((int64_t)j * a.nblk_max + (f >> 6) - blk_lo) * 16 + (f & 15);
+        } else {
+            return ((int64_t)j * a.BO + (o - obase)) * a.rank + r;
+        }
+    };
+    auto bfrag = [&](int p, int h, int g) __attribute__((always_inline)) -> Frag {
+        const int64_t o = obase + 32 * p + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+        const int gg = g < a.G ? g : 0;
+        const int j = gg / a.n_rg;
+        const int rr = (gg % a.n_rg) * 16 + 4 * gq;
+        const bool live = p < np && gslot[g] >= 0 && o < o_end && rr < a.rank;
+        Frag fr;
+        if constexpr (QUAD) {
+            fr = *reinterpret_cast<const Frag *>(bp + b_index(j, live ? o : obase, live ? rr : 0));
+            fr = live ? fr : Frag{};
+        } else {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool le = live && rr + e < a.rank;
+                const float t = DT<XT>::to_f32(bp[b_index(j, le ? o : obase, le ? rr + e : 0)]);
+                v[e] = le ? t : 0.0f;
+            }
+            if constexpr (sizeof(XT) == 2) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) fr[e] = __builtin_bit_cast(short, (__bf16)v[e]);
+            } else {
+                fr = f32x4{v[0], v[1], v[2], v[3]};
+            }
+        }
+        return fr;
+    };
+    auto compute = [&](const Frag *mf, int p, float vals[8]) __attribute__((always_inline)) {
         f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -448,12 +668,13 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
             for (int g = 0; g < GM; ++g) {
                 // a group without an adapter contributes exact zeros (its mid slot is not written)
                 const Frag m = gslot[g] >= 0 ? mf[g] : Frag{};
+                const Frag bf = bfrag(p, h, g);
                 if constexpr (sizeof(XT) == 2) {
-                    acc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bfr[p][h][g], m, acc[h], 0, 0, 0);
+                    acc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf, m, acc[h], 0, 0, 0);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        acc[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(bfr[p][h][g][e], m[e], acc[h], 0, 0, 0);
+                        acc[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[e], m[e], acc[h], 0, 0, 0);
                 }
             }
         }
@@ -463,86 +684,44 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
             vals[4 + e] = acc[1][e];
         }
     };
-    // mid fragments; groups without an adapter read group 0 of the same row (their B
-    // fragments are zero), so every lane issues the same unconditional loads.
-    int gsrc[GM];
-#pragma unroll
-    for (int g = 0; g < GM; ++g) gsrc[g] = gslot[g] >= 0 ? g : 0;
-    auto load_mid = [&](int64_t row, Frag *mf) {
+
+    // ---- sub-tiles: 16 tokens per wave each. Every load of a sub-tile is issued up front
+    // (rows and columns clamped in range); waves of other workgroups hide the latency.
+    const int64_t omax = a.d_out - 8;
+    for (int sub = 0; sub < a.subs_e; ++sub) {
+        // keeps the B fragment reads inside the loop (read from LDS per use, not held in registers)
+        asm volatile("" ::: "memory");
+        bool valid;
+        const int64_t row = sub_row(sub, valid);
+        Frag mf[GM];
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
             const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + gsrc[g] * 16 + 4 * gq;
             if constexpr (sizeof(XT) == 2) mf[g] = *reinterpret_cast<const i16x4 *>(src);
             else mf[g] = *reinterpret_cast<const f32x4 *>(src);
         }
-    };
-
-    if (a.vec_y) {
-        // Vector path: every load is unconditional (rows and columns clamped in range).
-        // Two sub-tile buffers ping-pong: the next sub-tile's mid and y loads are in
-        // flight while the current one computes and stores; with no next sub-tile they
-        // read one dummy address, so no branch separates a load from its use.
-        const int64_t omax = a.d_out - 8;
-        const YT *ydummy = static_cast<const YT *>(a.y);
-        const XT *mdummy = static_cast<const XT *>(a.mid);
-        struct Sub {
-            int64_t row;
-            bool valid;
-            Frag mf[GM];
+        YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
+        if (a.vec_y) {
             Y8<YT> yv[NP];
-        };
-        auto load_sub = [&](Sub &t, int sub, bool real) {
-            t.row = sub_row(real ? sub : 0, t.valid);
-            t.valid = t.valid && real;
-#pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                const XT *src = real ? static_cast<const XT *>(a.mid) + t.row * a.MR + gsrc[g] * 16 + 4 * gq : mdummy;
-                if constexpr (sizeof(XT) == 2) t.mf[g] = *reinterpret_cast<const i16x4 *>(src);
-                else t.mf[g] = *reinterpret_cast<const f32x4 *>(src);
-            }
             if constexpr (ACC) {
 #pragma unroll
                 for (int p = 0; p < NP; ++p)
-                    if (p < np)
-                        t.yv[p].load(real ? static_cast<const YT *>(a.y) + t.row * a.d_out +
-                                                std::min<int64_t>(obase + 32 * p + 8 * gq, omax)
-                                          : ydummy);
+                    if (p < np) yv[p].load(yr + std::min<int64_t>(obase + 32 * p + 8 * gq, omax));
             }
-        };
-        auto process = [&](const Sub &t) {
-            YT *yr = static_cast<YT *>(a.y) + t.row * a.d_out;
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 if (p >= np) break;
                 float vals[8];
-                compute(t.mf, p, vals);
+                compute(mf, p, vals);
                 const int64_t o8 = obase + 32 * p + 8 * gq;
                 Y8<YT> out;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    out.set(e, finish<YT>(vals[e], s_b, ACC ? t.yv[p].get(e) : 0.0f, ACC));
-                if (t.valid && o8 < a.d_out) out.store(yr + o8);
+                    out.set(e, finish<YT>(vals[e], s_b, ACC ? yv[p].get(e) : 0.0f, ACC));
+                if (valid && o8 < a.d_out) out.store(yr + o8);
             }
-        };
-        Sub ta, tb;
-        load_sub(ta, 0, true);
-        for (int sub = 0; sub < a.subs_e; sub += 2) {
-            load_sub(tb, sub + 1, sub + 1 < a.subs_e);
-            __builtin_amdgcn_sched_barrier(0);
-            process(ta);
-            if (sub + 1 >= a.subs_e) break;
-            load_sub(ta, sub + 2, sub + 2 < a.subs_e);
-            __builtin_amdgcn_sched_barrier(0);
-            process(tb);
-        }
-    } else {
-        // Element path for d_out not a multiple of 8 (rows not 16-byte aligned).
-        for (int sub = 0; sub < a.subs_e; ++sub) {
-            bool valid;
-            const int64_t row = sub_row(sub, valid);
-            Frag mf[GM];
-            load_mid(row, mf);
-            YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
+        } else {
+            // element path for d_out not a multiple of 8 (rows not 16-byte aligned)
             for (int p = 0; p < np; ++p) {
                 float vals[8];
                 compute(mf, p, vals);
@@ -568,11 +747,10 @@ int env_int(const char *name, int dflt) {
 
 struct Plan {
     int G, n_rg, GM, MR;
-    int tiles_s, ks, Kc, arow, red_off;
-    size_t lds_s;
-    int tiles_e, subs_e, BO, BOM, U;
-    int64_t nb_a_route, nb_b_route;
-    int64_t off_mid, off_pa, off_pb, total;
+    int tiles_s, ks, pb, arow, region, red_off;
+    size_t lds_s, lds_e;
+    int tiles_e, subs_e, BO, BOM, U, nblk_max;
+    int64_t off_mid, total;
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -598,19 +776,23 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.ks = ks;
     const int tgw = kWaves / ks;
     p.tiles_s = (int)std::max<int64_t>(1, (seq + 16 * tgw - 1) / (16 * tgw));
-    // LDS chunk of A: GM*16 rows; periods (16 values per 64 k) or dense rows (one value per k)
+    // Ring of two LDS regions, each holding the GM*16 factor rows of one K piece of pb blocks:
+    // periods (16 values per block; the plan keeps a piece's items within one fill batch) or
+    // dense rows (64 values per block).
     const int pad = 16 / xbytes;
-    const int budget = env_int("LITHE_CHUNK_LDS", 26 * 1024);
-    int64_t kc = dense ? ((budget / (p.GM * 16 * xbytes) - pad) / 64) * 64
-                       : ((budget / (p.GM * 16 * xbytes) - pad) / 16) * 64;
-    kc = std::max<int64_t>(64, kc);
-    const int64_t nb_total = d_in / kBlock;
-    const int64_t nchunk = (d_in + kc - 1) / kc;
-    const int64_t nbc = (nb_total + nchunk - 1) / nchunk;     // balanced chunks
-    p.Kc = (int)(nbc * kBlock);
-    p.arow = dense ? (int)(p.Kc + pad) : (int)(nbc * 16 + pad);
-    const size_t chunk_bytes = (size_t)p.GM * 16 * p.arow * xbytes;
-    p.red_off = (int)((chunk_bytes + 15) & ~size_t(15));
+    if (dense) {
+        p.pb = std::max(1, 4 / p.GM);
+        p.arow = p.pb * kBlock + pad;
+    } else {
+        p.pb = std::max(1, std::min(16, kFillBatch * kThreads / (p.GM * 16)));
+        p.arow = p.pb * 16 + pad;
+    }
+    if (getenv("LITHE_SHRINK_PB") && !dense) {
+        p.pb = std::max(1, std::min(env_int("LITHE_SHRINK_PB", p.pb), kFillBatch * kThreads / (p.GM * 16)));
+        p.arow = p.pb * 16 + pad;
+    }
+    p.region = p.GM * 16 * p.arow;
+    p.red_off = kHead + 2 * p.region * xbytes;
     p.lds_s = p.red_off + (ks > 1 ? (size_t)kWaves * p.GM * 64 * 16 : 0);
 
     // expand: BO outputs x 64*subs tokens per workgroup.
@@ -626,34 +808,29 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
+    // B periods of one output tile: the blocks covering outputs [obase, obase + BO) of a route
+    p.nblk_max = (int)(((int64_t)p.BO * rank + kBlock - 1) / kBlock + 1);
+    p.lds_e = kHead + (dense ? (size_t)n_route * p.BO * rank * xbytes : (size_t)n_route * p.nblk_max * 16 * xbytes);
 
-    // workspace: [error word | mid | A periods | B periods]
-    p.nb_a_route = (int64_t)p.n_rg * 16 * (d_in / kBlock);
-    p.nb_b_route = (d_out * rank) / kBlock;
+    // workspace: [error word | mid]
     p.off_mid = 256;
-    p.off_pa = align256(p.off_mid + rows * p.MR * xbytes);
-    const int64_t pa_bytes = dense ? 0 : n_batch * n_route * p.nb_a_route * 16 * xbytes;
-    const int64_t pb_bytes = dense ? 0 : n_batch * n_route * p.nb_b_route * 16 * xbytes;
-    p.off_pb = align256(p.off_pa + pa_bytes);
-    p.total = align256(p.off_pb + pb_bytes);
+    p.total = align256(p.off_mid + rows * p.MR * xbytes);
     return p;
 }
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, int U>
 void launch(const Plan &p, LoraArgs &a, hipStream_t st) {
-    if constexpr (SRC == SRC_INDEXED) {
-        const int64_t na = a.n_batch * a.n_route * a.nb_a_route;
-        const int64_t nitems = na + a.n_batch * a.n_route * a.nb_b_route;
-        hipLaunchKernelGGL((decode_periods_kernel<XT>), dim3((unsigned)((nitems + kThreads - 1) / kThreads)),
-                           dim3(kThreads), 0, st, a, na, nitems);
-    }
     hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, U>), dim3((unsigned)(a.n_batch * p.tiles_s)), dim3(kThreads),
                        p.lds_s, st, a);
     dim3 ge((unsigned)(((a.d_out + p.BO - 1) / p.BO) * a.n_batch * p.tiles_e));
-    if (a.accumulate)
-        hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true>), ge, dim3(kThreads), 0, st, a);
-    else
-        hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false>), ge, dim3(kThreads), 0, st, a);
+    const bool quad = (a.rank & 3) == 0;
+    if (a.accumulate) {
+        if (quad) hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), p.lds_e, st, a);
+        else hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, false>), ge, dim3(kThreads), p.lds_e, st, a);
+    } else {
+        if (quad) hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false, true>), ge, dim3(kThreads), p.lds_e, st, a);
+        else hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false, false>), ge, dim3(kThreads), p.lds_e, st, a);
+    }
 }
 
 template <typename XT, typename YT, int SRC>
@@ -693,7 +870,6 @@ extern "C" int64_t lithe_lora_workspace_bytes(int64_t n_batch, int64_t seq, int6
     if (x_dtype != LITHE_DT_BF16 && x_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
     const int n_rg = (rank + 15) / 16;
     if (n_rg * n_route > kMaxGroups) return LITHE_ERR_SHAPE;
-    // The indexed plan needs the period buffers, so it bounds the dense one.
     return make_plan(n_batch, seq, d_in, d_out, rank, n_route, x_dtype == LITHE_DT_BF16 ? 2 : 4, false).total;
 }
 
@@ -741,7 +917,8 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
         if (!f->dense_a || !f->dense_b) return LITHE_ERR_NULL;
         if (f->dense_dtype != x_dtype) return LITHE_ERR_DTYPE;
         if (f->n_dense < 1) return LITHE_ERR_SHAPE;
-        if ((uintptr_t)f->dense_a & 15u) return LITHE_ERR_ALIGN;
+        if (((uintptr_t)f->dense_a & 15u) || ((uintptr_t)f->dense_b & 15u)) return LITHE_ERR_ALIGN;
+        if (routes->weight_sqrt || routes->slot_scale) return LITHE_ERR_UNSUPPORTED;
         a.dense_a = f->dense_a;
         a.dense_b = f->dense_b;
         a.n_slots = f->n_dense;
@@ -757,15 +934,11 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     a.y = y;
     a.err = reinterpret_cast<int32_t *>(ws);
     a.mid = ws + p.off_mid;
-    a.pat_a = ws + p.off_pa;
-    a.pat_b = ws + p.off_pb;
     a.n_batch = n_batch;
     a.seq = seq;
     a.d_in = d_in;
     a.d_out = d_out;
     a.rows = n_batch * seq;
-    a.nb_a_route = p.nb_a_route;
-    a.nb_b_route = p.nb_b_route;
     a.rank = rank;
     a.G = p.G;
     a.n_rg = p.n_rg;
@@ -773,12 +946,14 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     a.MR = p.MR;
     a.tiles_s = p.tiles_s;
     a.ks = p.ks;
-    a.Kc = p.Kc;
+    a.pb = p.pb;
     a.arow = p.arow;
+    a.region = p.region;
     a.red_off = p.red_off;
     a.tiles_e = p.tiles_e;
     a.subs_e = p.subs_e;
     a.BO = p.BO;
+    a.nblk_max = p.nblk_max;
     a.vec_y = (d_out % 8 == 0) && (((uintptr_t)y & 15u) == 0);
     a.accumulate = accumulate ? 1 : 0;
     a.out_scale = out_scale;

@@ -25,8 +25,8 @@ LIB_PATH = os.path.join(_PKG, "_lib", "liblithe_amd.so")
 
 # ------------------------------------------------------------------ C constants (lithe_amd.h)
 OK = 0
-ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_RANGE, ERR_WORKSPACE, ERR_HIP, ERR_LEVELS = (
-    -1, -2, -3, -4, -5, -6, -7, -8)
+ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_RANGE, ERR_WORKSPACE, ERR_HIP, ERR_LEVELS, ERR_UNSUPPORTED = (
+    -1, -2, -3, -4, -5, -6, -7, -8, -9)
 DT_BF16, DT_F32, DT_F16, DT_I16, DT_I32, DT_I64, DT_U16 = 1, 2, 3, 4, 5, 6, 7
 IDX_PACKED9, IDX_LEVEL_I32, IDX_LEVEL_I16, IDX_BLOCK_I16 = 1, 2, 3, 4
 FACTOR_INDEXED, FACTOR_DENSE = 1, 2
