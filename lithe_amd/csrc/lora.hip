@@ -467,7 +467,7 @@ template <> struct Y8<float> {
 };
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
-__global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
+__device__ __forceinline__ void expand_body(const LoraArgs &a) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
     const int tid = threadIdx.x;
@@ -737,6 +737,18 @@ __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
     }
 }
 
+// Two entry points of one body: the second asks the compiler for 4 waves per SIMD (at most
+// 128 VGPRs); it is used where the body fits that budget without spilling (one rank group,
+// bf16 output).
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+__global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a);
+}
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) expand_kernel_w4(LoraArgs a) {
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a);
+}
+
 // ============================================================================ host plan
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
@@ -768,7 +780,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // shrink: one wave per 16 tokens x (K / ks); ks grows until there are enough waves.
     const int64_t groups = n_batch * ((seq + 15) / 16);
     int ks = 1;
-    while (ks < 4 && groups * ks < target) ks *= 2;
+    while (ks < 4 && (groups * ks < target || d_in / ks > 6144)) ks *= 2;   // long K: shorter per-wave streams
     if (getenv("LITHE_SHRINK_KS")) {
         const int v = env_int("LITHE_SHRINK_KS", ks);
         ks = v >= 4 ? 4 : v >= 2 ? 2 : 1;
@@ -804,7 +816,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);
     const int64_t o_tiles = (d_out + p.BO - 1) / p.BO;
     const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
-    int subs = (int)std::max<int64_t>(1, std::min<int64_t>(4, base_wgs / (2 * target)));
+    int subs = base_wgs >= 4 * 256 ? 2 : 1;    // 2 sub-tiles of 64 tokens: measured best at every FLUX shape
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
@@ -824,6 +836,15 @@ void launch(const Plan &p, LoraArgs &a, hipStream_t st) {
                        p.lds_s, st, a);
     dim3 ge((unsigned)(((a.d_out + p.BO - 1) / p.BO) * a.n_batch * p.tiles_e));
     const bool quad = (a.rank & 3) == 0;
+    if constexpr (GM == 1 && sizeof(YT) == 2) {
+        if (quad) {
+            if (a.accumulate)
+                hipLaunchKernelGGL((expand_kernel_w4<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), p.lds_e, st, a);
+            else
+                hipLaunchKernelGGL((expand_kernel_w4<XT, YT, SRC, GM, BOM, false, true>), ge, dim3(kThreads), p.lds_e, st, a);
+            return;
+        }
+    }
     if (a.accumulate) {
         if (quad) hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), p.lds_e, st, a);
         else hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, false>), ge, dim3(kThreads), p.lds_e, st, a);

@@ -1,0 +1,196 @@
+"""CPU checks of the C ABI: the library loads, exports every function include/lithe_amd.h
+declares with the signature the ctypes binding uses, and rejects bad arguments before any
+GPU work (no call here reaches a kernel launch).
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from lithe_amd.kernels import _hip
+from oracle import packing as opk
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lithe_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lithe_[a-z0-9_]+)\s*\(", text)))
+
+
+def _defines():
+    return {m.group(1): int(m.group(2)) for m in re.finditer(r"#define\s+(LITHE_\w+)\s+(-?\d+)", open(HEADER).read())}
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _hip.load()
+    names = _declared()
+    assert len(names) >= 9, names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in lithe_amd.h but not exported"
+        assert n in _hip.SIGNATURES, f"{n} has no ctypes signature in _hip.SIGNATURES"
+    assert sorted(_hip.SIGNATURES) == names
+
+
+def test_constants_match_header():
+    d = _defines()
+    assert d["LITHE_OK"] == _hip.OK
+    for n in ("NULL", "SHAPE", "ALIGN", "DTYPE", "RANGE", "WORKSPACE", "HIP", "LEVELS", "UNSUPPORTED"):
+        assert d[f"LITHE_ERR_{n}"] == getattr(_hip, f"ERR_{n}"), n
+    for n in ("BF16", "F32", "F16", "I16", "I32", "I64", "U16"):
+        assert d[f"LITHE_DT_{n}"] == getattr(_hip, f"DT_{n}"), n
+    for n in ("PACKED9", "LEVEL_I32", "LEVEL_I16", "BLOCK_I16"):
+        assert d[f"LITHE_IDX_{n}"] == getattr(_hip, f"IDX_{n}"), n
+    assert d["LITHE_FACTOR_INDEXED"] == _hip.FACTOR_INDEXED and d["LITHE_FACTOR_DENSE"] == _hip.FACTOR_DENSE
+
+
+def test_struct_layouts_match_header_sizes():
+    # lithe_index_src: ptr, 2 x int32, 4 x int64 ; lithe_lut: int32 + 40 floats ; routes: 3 ptrs + int32
+    assert ctypes.sizeof(_hip.IndexSrc) == 8 + 4 + 4 + 4 * 8
+    assert ctypes.sizeof(_hip.Lut) == 4 + 40 * 4
+    assert ctypes.sizeof(_hip.Routes) == 3 * 8 + 8
+    assert _hip.Factors.a_idx.offset == 8 and _hip.Factors.dense_a.offset % 8 == 0
+
+
+def test_version_and_status_strings():
+    lib = _hip.load()
+    assert lib.lithe_abi_version() == 1
+    for code in range(0, -10, -1):
+        s = lib.lithe_status_string(code).decode()
+        assert s and "unknown" not in s.lower(), (code, s)
+    assert "unknown" in lib.lithe_status_string(-99).decode().lower()
+
+
+@pytest.mark.parametrize("n", [0, 1, 6, 7, 8, 700, 1001, 100_003])
+def test_host_pack_matches_oracle(n):
+    lib = _hip.load()
+    v = np.random.default_rng(n).integers(0, 512, n).astype(np.uint16)
+    words = np.zeros(max(1, -(-n // 7)), dtype=np.uint64)
+    rc = lib.lithe_pack9_host(v.ctypes.data, n, words.ctypes.data)
+    assert rc == _hip.OK
+    assert np.array_equal(words[: -(-n // 7)], opk.pack(v))
+
+
+def test_host_pack_rejects_512():
+    lib = _hip.load()
+    v = np.array([1, 2, 512, 3], dtype=np.uint16)
+    words = np.zeros(1, dtype=np.uint64)
+    assert lib.lithe_pack9_host(v.ctypes.data, 4, words.ctypes.data) == _hip.ERR_RANGE
+    assert lib.lithe_pack9_host(None, 4, words.ctypes.data) == _hip.ERR_NULL
+
+
+def test_workspace_bytes():
+    lib = _hip.load()
+    ws = lib.lithe_lora_workspace_bytes
+    # head + mid (rows x 16 x 2 B), 256-aligned
+    n = ws(14, 4608, 3072, 3072, 16, 1, _hip.DT_BF16)
+    assert n == 256 + ((14 * 4608 * 16 * 2 + 255) // 256) * 256
+    assert ws(2, 3, 64, 64, 16, 1, _hip.DT_F32) >= 256 + 2 * 3 * 16 * 4
+    # two rank groups per route entry, four entries
+    assert ws(1, 10, 128, 64, 32, 4, _hip.DT_BF16) >= 256 + 10 * 128 * 2
+    assert ws(1, 10, 128, 64, 16, 9, _hip.DT_BF16) == _hip.ERR_SHAPE     # 9 groups > 8
+    assert ws(1, 10, 32, 64, 16, 1, _hip.DT_BF16) == _hip.ERR_SHAPE      # d_in < 64
+    assert ws(1, 10, 128, 64, 16, 1, _hip.DT_F16) == _hip.ERR_DTYPE
+
+
+def _indexed(levels=3, n_slots=4, d_in=128, d_out=64, rank=16):
+    nb = rank * d_in // 64 + d_out * rank // 64
+    words = np.zeros((n_slots, -(-nb * levels // 7)), dtype=np.uint64)
+    src = _hip.IndexSrc(base=words.ctypes.data, kind=_hip.IDX_PACKED9, num_levels=levels,
+                        slot_stride=words.shape[1], level_stride=0, block_off=0, n_slots=n_slots)
+    srcb = _hip.IndexSrc(base=words.ctypes.data, kind=_hip.IDX_PACKED9, num_levels=levels,
+                         slot_stride=words.shape[1], level_stride=0, block_off=rank * d_in // 64, n_slots=n_slots)
+    f = _hip.Factors()
+    f.kind = _hip.FACTOR_INDEXED
+    f.a_idx, f.b_idx = src, srcb
+    f.lut_a.num_levels = f.lut_b.num_levels = levels
+    return f, words
+
+
+def _delta(lib, f, route, *, x=1 << 12, y=1 << 12, ws=1 << 12, x_dt=None, y_dt=None, n_batch=2, seq=8,
+           d_in=128, d_out=64, rank=16, wsb=1 << 20, dense=False):
+    return lib.lithe_lora_delta(ctypes.c_void_p(x), x_dt or _hip.DT_BF16, n_batch, seq, d_in, ctypes.c_void_p(y),
+                                y_dt or _hip.DT_BF16, d_out, 1, rank, ctypes.byref(f) if f else None,
+                                ctypes.byref(route) if route else None, None, ctypes.c_float(1.0), None,
+                                ctypes.c_void_p(ws), wsb, None)
+
+
+def test_delta_argument_errors_before_any_launch():
+    """Every case fails validation on the host; fake (aligned, never dereferenced) pointers suffice."""
+    lib = _hip.load()
+    f, words = _indexed()
+    slot = np.zeros(2, dtype=np.int32)
+    route = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=None, slot_scale=None, n_route=1)
+    assert _delta(lib, None, route) == _hip.ERR_NULL
+    assert _delta(lib, f, None) == _hip.ERR_NULL
+    assert _delta(lib, f, route, x_dt=_hip.DT_F16) == _hip.ERR_DTYPE
+    assert _delta(lib, f, route, y_dt=_hip.DT_I32) == _hip.ERR_DTYPE
+    assert _delta(lib, f, route, d_in=100) == _hip.ERR_ALIGN                # d_in % 64
+    assert _delta(lib, f, route, d_out=60, rank=1) == _hip.ERR_ALIGN        # d_out * rank % 64
+    assert _delta(lib, f, route, n_batch=-1) == _hip.ERR_SHAPE
+    assert _delta(lib, f, route, rank=0) == _hip.ERR_SHAPE
+    assert _delta(lib, f, route, n_batch=0) == _hip.OK                      # empty batch: nothing to do
+    assert _delta(lib, f, route, x=0) == _hip.ERR_NULL
+    assert _delta(lib, f, route, ws=0) == _hip.ERR_WORKSPACE
+    assert _delta(lib, f, route, x=(1 << 12) + 8) == _hip.ERR_ALIGN         # x not 16-byte aligned
+    assert _delta(lib, f, route, ws=(1 << 12) + 16) == _hip.ERR_ALIGN       # workspace not 256-aligned
+    assert _delta(lib, f, route, wsb=256) == _hip.ERR_WORKSPACE             # too small
+    # index sources: levels must agree, and cover the factor
+    f2, _ = _indexed()
+    f2.lut_b.num_levels = 2
+    assert _delta(lib, f2, route) == _hip.ERR_LEVELS
+    assert _delta(lib, f, route, d_in=256) == _hip.ERR_SHAPE                # A extends past the slot
+    f3, _ = _indexed()
+    f3.a_idx.num_levels = 5
+    assert _delta(lib, f3, route) == _hip.ERR_LEVELS
+    f4, _ = _indexed()
+    f4.a_idx.kind = 9
+    assert _delta(lib, f4, route) == _hip.ERR_DTYPE
+    # route weights are for indexed factors only
+    a = np.zeros(16, dtype=np.uint16)
+    fd = _hip.Factors()
+    fd.kind = _hip.FACTOR_DENSE
+    fd.dense_dtype = _hip.DT_BF16
+    fd.dense_a, fd.dense_b, fd.n_dense = 1 << 12, 1 << 13, 2
+    w = np.ones(2, dtype=np.float32)
+    rw = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=w.ctypes.data, slot_scale=None, n_route=1)
+    assert _delta(lib, fd, rw) == _hip.ERR_UNSUPPORTED
+    fd.dense_dtype = _hip.DT_F32
+    assert _delta(lib, fd, route) == _hip.ERR_DTYPE                          # dense dtype != x dtype
+    del a, words
+
+
+def test_unpack_decode_argument_errors():
+    lib = _hip.load()
+    assert lib.lithe_unpack9(None, 5, ctypes.c_void_p(1 << 12), _hip.DT_I64, None) == _hip.ERR_NULL
+    assert lib.lithe_unpack9(ctypes.c_void_p(1 << 12), 5, ctypes.c_void_p(1 << 12), _hip.DT_BF16, None) == _hip.ERR_DTYPE
+    assert lib.lithe_unpack9(ctypes.c_void_p(1 << 12), -1, ctypes.c_void_p(1 << 12), _hip.DT_I64, None) == _hip.ERR_SHAPE
+    assert lib.lithe_unpack9(None, 0, None, _hip.DT_I64, None) == _hip.OK
+    lut = _hip.Lut(num_levels=3)
+    src = _hip.IndexSrc(base=1 << 12, kind=_hip.IDX_PACKED9, num_levels=3, slot_stride=10, level_stride=0,
+                        block_off=0, n_slots=1)
+    dec = lib.lithe_decode
+    assert dec(None, None, 1, 4, None, ctypes.byref(lut), ctypes.byref(lut), ctypes.c_void_p(1 << 12),
+               _hip.DT_BF16, 0, None, None) == _hip.ERR_NULL
+    assert dec(ctypes.byref(src), None, 1, 4, None, ctypes.byref(lut), ctypes.byref(lut), ctypes.c_void_p(1 << 12),
+               _hip.DT_I32, 0, None, None) == _hip.ERR_DTYPE
+    assert dec(ctypes.byref(src), None, 1, 1000, None, ctypes.byref(lut), ctypes.byref(lut),
+               ctypes.c_void_p(1 << 12), _hip.DT_BF16, 0, None, None) == _hip.ERR_SHAPE   # 1000 blocks > slot
+
+
+def test_product_entry_points_refuse_cpu_tensors():
+    import lithe_amd
+    from lithe_amd.kernels import decode_packed, pack_adapter, unpack_indices
+    from helpers import SMALL, random_adapter
+    ad = random_adapter(SMALL, rank=16, seed=0)
+    words, layout = pack_adapter(ad)
+    pa, pb = lithe_amd.twin_pools()
+    with pytest.raises(RuntimeError):
+        decode_packed(words, layout, pa, pb)
+    with pytest.raises(RuntimeError):
+        unpack_indices(words.view(torch.int64), 7)
