@@ -56,7 +56,7 @@ typedef struct lithe_index_src {
     const void *base;       /* device pointer */
     int32_t kind;           /* LITHE_IDX_* */
     int32_t num_levels;     /* 1..4 */
-    int64_t slot_stride;    /* elements (uint64 words for PACKED9) from one slot to the next */
+    int64_t slot_stride;    /* elements (uint64 words for PACKED9, < 2^32 / 7) from one slot to the next */
     int64_t level_stride;   /* elements from one level to the next (LEVEL_* kinds only) */
     int64_t block_off;      /* first block of the factor inside a slot (a_off / b_off of the layout) */
     int64_t n_slots;        /* number of addressable slots; larger slot ids are rejected in-kernel */

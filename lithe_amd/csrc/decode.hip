@@ -140,6 +140,8 @@ int32_t check_src(const lithe_index_src *s) {
     if (s->kind < LITHE_IDX_PACKED9 || s->kind > LITHE_IDX_BLOCK_I16) return LITHE_ERR_DTYPE;
     if (s->slot_stride < 0 || s->level_stride < 0 || s->block_off < 0 || s->n_slots < 1)
         return LITHE_ERR_SHAPE;
+    // packed positions inside one slot are 32-bit in the kernels
+    if (s->kind == LITHE_IDX_PACKED9 && s->slot_stride >= ((int64_t)1 << 32) / 7) return LITHE_ERR_SHAPE;
     return LITHE_OK;
 }
 

@@ -63,18 +63,21 @@ struct RawIdx {
 // Loads the raw index data of NQ blocks. The kind switch sits outside the block loop and
 // every load is unconditional, so all NQ blocks' loads issue back to back and nothing
 // waits for them until extract_indices() reads the registers.
-template <int NQ>
+// PK: the source is known to be PACKED9 (the kernels' fast path); no kind dispatch is emitted.
+template <int NQ, bool PK = false, int LV = 0>
 __device__ __forceinline__ void load_raw(const IdxSrc &s, const int64_t slot[NQ], const int64_t block[NQ],
                                          RawIdx r[NQ]) {
-    const int L = s.levels;
-    switch (s.kind) {
+    const int L = LV > 0 ? LV : s.levels;
+    switch (PK ? LITHE_IDX_PACKED9 : s.kind) {
         case LITHE_IDX_PACKED9:
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
+                // positions inside a slot fit 32 bits (the host checks slot_stride * 7 < 2^32),
+                // so / 7 is a multiply-high, not a 64-bit division routine
                 const uint64_t *w = static_cast<const uint64_t *>(s.base) + slot[q] * s.slot_stride;
-                const int64_t p0 = (s.block_off + block[q]) * L;
-                const uint64_t lo = w[p0 / 7];
-                const uint64_t hi = w[(p0 + L - 1) / 7];
+                const uint32_t p0 = (uint32_t)(s.block_off + block[q]) * (uint32_t)L;
+                const uint64_t lo = w[p0 / 7u];
+                const uint64_t hi = w[(p0 + (uint32_t)L - 1u) / 7u];
                 r[q].v[0] = (uint32_t)lo;
                 r[q].v[1] = (uint32_t)(lo >> 32);
                 r[q].v[2] = (uint32_t)hi;
@@ -110,19 +113,21 @@ __device__ __forceinline__ void load_raw(const IdxSrc &s, const int64_t slot[NQ]
 
 // The L indices of block `block` from its raw data. Returns false when an index read from
 // an unpacked source is out of range (it is then replaced by 0).
+template <bool PK = false, int LV = 0>
 __device__ __forceinline__ bool extract_indices(const IdxSrc &s, int64_t block, const RawIdx &r,
                                                 uint32_t k[kMaxLevels]) {
-    const int L = s.levels;
-    if (s.kind == LITHE_IDX_PACKED9) {
-        const int64_t p0 = (s.block_off + block) * L;
-        const int64_t w0 = p0 / 7;
+    const int L = LV > 0 ? LV : s.levels;
+    if (PK || s.kind == LITHE_IDX_PACKED9) {
+        const uint32_t p0 = (uint32_t)(s.block_off + block) * (uint32_t)L;
+        const uint32_t w0 = p0 / 7u;
         const uint64_t lo = (uint64_t)r.v[0] | ((uint64_t)r.v[1] << 32);
         const uint64_t hi = (uint64_t)r.v[2] | ((uint64_t)r.v[3] << 32);
 #pragma unroll
         for (int l = 0; l < kMaxLevels; ++l) {
-            const int64_t p = p0 + l;
-            const uint64_t word = (p / 7 == w0) ? lo : hi;
-            k[l] = l < L ? (uint32_t)(word >> (9 * (int)(p % 7))) & kIndexMask : 0u;
+            const uint32_t p = p0 + (uint32_t)l;
+            const uint32_t wq = p / 7u;
+            const uint64_t word = (wq == w0) ? lo : hi;
+            k[l] = l < L ? (uint32_t)(word >> (9u * (p - 7u * wq))) & kIndexMask : 0u;
         }
         return true;
     }
@@ -149,13 +154,15 @@ __device__ __forceinline__ bool fetch_indices(const IdxSrc &s, int64_t slot, int
 }
 
 // Decoded value at period position t (mask m = sign_mask(t)) from the L indices,
-// summed in level order in fp32: (v0 + v1) + v2 (+ v3).
+// summed in level order in fp32: (v0 + v1) + v2 (+ v3). LV > 0 fixes L = LV at compile
+// time (branch-free: every table lookup of a block can be in flight at once); LV = 0 reads L.
+template <int LV = 0>
 __device__ __forceinline__ float decode_value(const float *lut /* [levels][10] in LDS */, int L,
                                               const uint32_t k[kMaxLevels], uint32_t m) {
     float v = lut[__builtin_popcount((k[0] ^ m) & kIndexMask)];
 #pragma unroll
     for (int l = 1; l < kMaxLevels; ++l)
-        if (l < L) v += lut[l * 10 + __builtin_popcount((k[l] ^ m) & kIndexMask)];
+        if (LV > 0 ? l < LV : l < L) v += lut[l * 10 + __builtin_popcount((k[l] ^ m) & kIndexMask)];
     return v;
 }
 

@@ -56,7 +56,12 @@ constexpr int kHead = 256;
 static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
 constexpr int kFillBatch = 2;     // fill items per thread whose loads are issued together
 
-enum { SRC_INDEXED = 1, SRC_DENSE = 2 };
+// Factor sources: SRC_PACKED is SRC_INDEXED with both index streams PACKED9 with 3 levels (the
+// resident bank of the twin codebook), compiled without the kind dispatch of the other index
+// layouts and with the level count fixed.
+enum { SRC_INDEXED = 1, SRC_DENSE = 2, SRC_PACKED = 3 };
+constexpr int kPackedLevels = 3;
+template <int SRC> constexpr int fixed_levels() { return SRC == SRC_PACKED ? kPackedLevels : 0; }
 
 struct LoraArgs {
     const void *x;
@@ -185,7 +190,13 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
         for (int q = 1; q < GM; ++q) r = g == q ? gw[q] : r;
         return r;
     };
-    if constexpr (SRC == SRC_INDEXED) stage_lut(lut, a.luts.v[0][0], tid);
+    auto group_rank0 = [&](int g) __attribute__((always_inline)) -> int {   // (g % n_rg) * 16
+        int r = 0;
+#pragma unroll
+        for (int q = 1; q < GM; ++q) r = g == q ? (q % a.n_rg) * 16 : r;
+        return r;
+    };
+    if constexpr (SRC != SRC_DENSE) stage_lut(lut, a.luts.v[0][0], tid);
 
     const int nb = (int)(a.d_in / kBlock);
     const int pb = a.pb;
@@ -195,12 +206,13 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     // ---- fills. Indexed: item = the 16-value period of (row gr, block c) of piece g, at
     // most kFillBatch items per thread (the plan keeps GM * 16 * pb <= kFillBatch * kThreads);
     // the index loads of a piece are issued one piece ahead of its decode.
+    // item it of a piece: row gr = it % (GM*16), block c = it / (GM*16) (block-major: a shift)
+    constexpr int kRowsLog2 = GM == 1 ? 4 : GM == 2 ? 5 : GM == 4 ? 6 : 7;
     auto idx_item = [&](int g, int it, int &gr, int &c, bool &live) __attribute__((always_inline)) -> int64_t {
-        const int nbk = piece_blocks(g);
-        gr = it / nbk;
-        c = it - gr * nbk;
+        gr = it & (GM * 16 - 1);
+        c = it >> kRowsLog2;
         const int grp = gr >> 4;
-        const int rr = (grp % a.n_rg) * 16 + (gr & 15);
+        const int rr = group_rank0(grp) + (gr & 15);
         live = group_slot(grp) >= 0 && rr < a.rank;
         return live ? (int64_t)rr * nb + (int64_t)g * pb + c : 0;
     };
@@ -215,7 +227,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
             blk[q] = idx_item(g, std::min(q * kThreads + tid, items - 1), gr, c, live);
             slot[q] = live ? group_slot(gr >> 4) : 0;
         }
-        load_raw<kFillBatch>(a.a_src, slot, blk, dst);
+        load_raw<kFillBatch, SRC == SRC_PACKED, fixed_levels<SRC>()>(a.a_src, slot, blk, dst);
     };
     auto idx_store = [&](int g, const RawIdx *src) __attribute__((always_inline)) {
         if (g >= npiece) return;
@@ -229,12 +241,16 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
             bool live;
             const int64_t blk = idx_item(g, it, gr, c, live);
             uint32_t k[kMaxLevels];
-            const bool ok = extract_indices(a.a_src, blk, src[q], k);
+            const bool ok = extract_indices<SRC == SRC_PACKED, fixed_levels<SRC>()>(a.a_src, blk, src[q], k);
             if (live && !ok) record_error(a.err, kErrIndex);
             const float w = group_weight(gr >> 4);
             float v[16];
 #pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = live ? decode_value(lut, a.a_src.levels, k, sign_mask(t)) * w : 0.0f;
+            for (int t = 0; t < 16; ++t) {
+                // unconditional lookups, then a select: no branch between the table reads
+                const float d = decode_value<fixed_levels<SRC>()>(lut, a.a_src.levels, k, sign_mask(t)) * w;
+                v[t] = live ? d : 0.0f;
+            }
             store16<XT>(reg + gr * a.arow + c * 16, v);
             __builtin_amdgcn_sched_barrier(0);    // one item's values live at a time
         }
@@ -321,7 +337,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
                 const XT *ap;
-                if constexpr (SRC == SRC_INDEXED)
+                if constexpr (SRC != SRC_DENSE)
                     ap = reg + g * 16 * a.arow + (kBf16 ? ((sp + u) >> 1) * 16 + 8 * (gq & 1) : ((sp + u) >> 2) * 16 + 4 * gq);
                 else
                     ap = reg + g * 16 * a.arow + (sp + u) * KSTEP + (kBf16 ? 8 : 4) * gq;
@@ -348,7 +364,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     RawIdx raw[kFillBatch];
     {
         RawIdx raw1[kFillBatch];
-        if constexpr (SRC == SRC_INDEXED) {
+        if constexpr (SRC != SRC_DENSE) {
             idx_load(0, raw);
             idx_load(1, raw1);
         }
@@ -360,7 +376,8 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
         Batch ba, bb;
         load_batch(ba, da);
         load_batch(bb, db);
-        if constexpr (SRC == SRC_INDEXED) {
+        if constexpr (SRC != SRC_DENSE) {
+            __syncthreads();    // the value table staged by lane 0 is visible to every wave
             idx_store(0, raw);
             idx_store(1, raw1);
             idx_load(2, raw);
@@ -376,7 +393,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
         auto enter = [&](int g) __attribute__((always_inline)) {
             while (pg < g) {
                 __syncthreads();
-                if constexpr (SRC == SRC_INDEXED) {
+                if constexpr (SRC != SRC_DENSE) {
                     idx_store(pg + 2, raw);
                     idx_load(pg + 3, raw);
                 } else {
@@ -544,13 +561,13 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
     XT *bp = reinterpret_cast<XT *>(smem + kHead);
     const int64_t blk_lo = (obase * a.rank) >> 6;
     const int64_t o_end = std::min<int64_t>(obase + a.BO, a.d_out);
-    if constexpr (SRC == SRC_INDEXED) {
+    if constexpr (SRC != SRC_DENSE) {
         const int per_route = (int)(((o_end * a.rank + kBlock - 1) >> 6) - blk_lo) * 4;
         const int items = a.n_route * per_route;
         RawIdx raw[2];
         // block of item `it` inside the factor; 0 if its route entry is empty
         auto dec_block = [&](int it, int64_t &slot, float &w, float &sc) __attribute__((always_inline)) -> int64_t {
-            const int j = it / per_route;
+            const int j = a.n_route == 1 ? 0 : it / per_route;
             route_pick(j, slot, w, sc);
             const int64_t blk = blk_lo + ((it - j * per_route) >> 2);
             return slot >= 0 ? blk : 0;
@@ -563,27 +580,29 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
                 blk[q] = dec_block(std::min(base + q * kThreads + tid, items - 1), slot[q], w, sc);
                 slot[q] = slot[q] >= 0 ? slot[q] : 0;
             }
-            load_raw<2>(a.b_src, slot, blk, raw);
+            load_raw<2, SRC == SRC_PACKED, fixed_levels<SRC>()>(a.b_src, slot, blk, raw);
         };
         auto dec_store = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int it = base + q * kThreads + tid;
                 if (it >= items) break;
-                const int j = it / per_route;
+                const int j = a.n_route == 1 ? 0 : it / per_route;
                 const int rem = it - j * per_route;
                 const int blk = rem >> 2, qt = rem & 3;
                 int64_t slot;
                 float w, sc;
                 uint32_t k[kMaxLevels];
-                const bool ok = extract_indices(a.b_src, dec_block(it, slot, w, sc), raw[q], k);
+                const bool ok = extract_indices<SRC == SRC_PACKED, fixed_levels<SRC>()>(a.b_src, dec_block(it, slot, w, sc), raw[q], k);
                 const bool live = slot >= 0;
                 if (live && !ok) record_error(a.err, kErrIndex);
                 XT *dst = bp + ((int64_t)j * a.nblk_max + blk) * 16 + 4 * qt;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    v[e] = live ? (decode_value(lut, a.b_src.levels, k, sign_mask_rt(4 * qt + e)) * sc) * w : 0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    const float d = (decode_value<fixed_levels<SRC>()>(lut, a.b_src.levels, k, sign_mask_rt(4 * qt + e)) * sc) * w;
+                    v[e] = live ? d : 0.0f;
+                }
                 if constexpr (sizeof(XT) == 2) {
                     bf16x4 pk;
 #pragma unroll
@@ -626,7 +645,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
     // (rank % 4 == 0): the 4 ranks of a fragment are 4 consecutive LDS values, one 8-byte read
     // (fp32: 16 bytes); dead fragments read a valid address and are zeroed, without branches.
     auto b_index = [&](int j, int64_t o, int r) __attribute__((always_inline)) -> int64_t {
-        if constexpr (SRC == SRC_INDEXED) {
+        if constexpr (SRC != SRC_DENSE) {
             const int64_t f = o * a.rank + r;
             return ((int64_t)j * a.nblk_max + (f >> 6) - blk_lo) * 16 + (f & 15);
         } else {
@@ -810,8 +829,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // expand: BO outputs x 64*subs tokens per workgroup.
     int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
     bo_max = std::max(32, bo_max);
-    if (p.GM == 1 && env_int("LITHE_EXPAND_BO", 0) == 128) bo_max = 128;
-    p.U = (p.GM == 1 && env_int("LITHE_SHRINK_U", 4) == 8) ? 8 : 4;
+    p.U = 4;
     p.BOM = bo_max;
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);
     const int64_t o_tiles = (d_out + p.BO - 1) / p.BO;
@@ -858,15 +876,7 @@ template <typename XT, typename YT, int SRC>
 int32_t dispatch_gm(const Plan &p, LoraArgs &a, hipStream_t st) {
     constexpr bool bf = sizeof(XT) == 2;
     switch (p.GM) {
-        case 1:
-            if (p.U == 8) {
-                if (p.BOM == 128) launch<XT, YT, SRC, 1, 128, 8>(p, a, st);
-                else launch<XT, YT, SRC, 1, bf ? 256 : 128, 8>(p, a, st);
-            } else {
-                if (p.BOM == 128) launch<XT, YT, SRC, 1, 128, 4>(p, a, st);
-                else launch<XT, YT, SRC, 1, bf ? 256 : 128, 4>(p, a, st);
-            }
-            break;
+        case 1: launch<XT, YT, SRC, 1, bf ? 256 : 128, 4>(p, a, st); break;
         case 2: launch<XT, YT, SRC, 2, bf ? 256 : 128, 4>(p, a, st); break;
         case 4: launch<XT, YT, SRC, 4, bf ? 128 : 64, 4>(p, a, st); break;
         default: launch<XT, YT, SRC, 8, bf ? 64 : 32, 4>(p, a, st); break;
@@ -876,8 +886,10 @@ int32_t dispatch_gm(const Plan &p, LoraArgs &a, hipStream_t st) {
 
 template <typename XT, typename YT>
 int32_t dispatch_src(const Plan &p, LoraArgs &a, int kind, hipStream_t st) {
-    return kind == LITHE_FACTOR_DENSE ? dispatch_gm<XT, YT, SRC_DENSE>(p, a, st)
-                                      : dispatch_gm<XT, YT, SRC_INDEXED>(p, a, st);
+    if (kind == LITHE_FACTOR_DENSE) return dispatch_gm<XT, YT, SRC_DENSE>(p, a, st);
+    if (a.a_src.kind == LITHE_IDX_PACKED9 && a.b_src.kind == LITHE_IDX_PACKED9 && a.a_src.levels == kPackedLevels)
+        return dispatch_gm<XT, YT, SRC_PACKED>(p, a, st);
+    return dispatch_gm<XT, YT, SRC_INDEXED>(p, a, st);
 }
 
 }  // namespace
