@@ -10,7 +10,7 @@ inside the kernels. Inputs are synthetic (x, y ~ N(0, 1); uniformly random
 9-bit fields) and already resident in HBM; x / y buffers rotate so the 256 MB
 Infinity Cache cannot serve a module from a previous module's data.
 
-    python bench.py [--steps K] [--warmup W] [--config flux342|ffn|hb|decode]
+    python bench.py [--steps K] [--warmup W] [--config flux342|ffn|hb|decode] [--rank 16|64]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -226,12 +226,111 @@ def cpu_baseline(mods, batch, budget_s=25.0):
                       f"(d_in, d_out, tokens) classes, scaled by class count x batch {batch}"}
 
 
+def cpu_decode_baseline(layout, n_sample=2):
+    """Oracle C restatement of the bulk decode (OpenMP over the host cores), n_sample adapters."""
+    import numpy as np
+
+    from oracle import codebook as ocb
+    from oracle import native
+    pa, pb = ocb.twin_pools()
+    rng = np.random.default_rng(0)
+    n_idx = layout.num_indices
+    sides = layout.sides.numpy()
+    t = 0.0
+    for _ in range(n_sample):
+        words = native.pack(rng.integers(0, 512, n_idx).astype(np.uint16))
+        t0 = time.perf_counter()
+        native.decode(words, layout.total_blocks, layout.num_levels, sides, pa, pb, want="bf16")
+        t += time.perf_counter() - t0
+    per = t / n_sample
+    nbytes = layout.num_words * 8 + layout.total_blocks * 64 * 2
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "adapters_per_s": round(1.0 / per, 3),
+            "cores": int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0)))), "kind": "port",
+            "sample": f"oracle C decode (lo_decode, OpenMP) of {n_sample} packed adapters of the 342-linear "
+                      f"layout to bf16"}
+
+
+def run_decode(args):
+    """Bulk decode of a 10,000-adapter packed bank to dense bf16 A/B, chunked into a reused buffer."""
+    import torch
+
+    from lithe_amd.kernels import PackedBank, PackedLayout
+    rank = args.rank
+    dev = torch.device("cuda:0")
+    mods = flux_modules(4096, 512)
+    layout = PackedLayout.from_modules(
+        [{"name": n, "shape_a": [rank, di], "shape_b": [do, rank]} for n, di, do, _ in mods],
+        num_levels=3, block_size=64, scaling=1.0)
+    n_slots = args.slots or 10_000
+    bank = PackedBank(layout, dev, capacity=n_slots)
+    bank.fill_random(n_slots, generator=torch.Generator(device=dev).manual_seed(0))
+    out_per = layout.total_blocks * 64 * 2
+    in_per = layout.num_words * 8
+    chunk = max(1, min(n_slots, (6 << 30) // out_per))     # ~6 GB output buffer, reused
+    out = torch.empty((chunk, layout.total_blocks, 64), dtype=torch.bfloat16, device=dev)
+    chunks = [torch.arange(s, min(n_slots, s + chunk), dtype=torch.int32, device=dev)
+              for s in range(0, n_slots, chunk)]
+
+    def step():
+        for c in chunks:
+            bank.decode_slots(c, out=out[: c.numel()])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(args.steps):
+        step()
+    e.record(stream)
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    # per-launch duration of the full chunks, HIP events on the launch stream
+    full = [c for c in chunks if c.numel() == chunk]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(full) + 1)]
+    ev[0].record(stream)
+    for i, c in enumerate(full):
+        bank.decode_slots(c, out=out)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    launch_ms = sum(ev[i].elapsed_time(ev[i + 1]) for i in range(len(full))) / len(full)
+    launch_bytes = chunk * (in_per + out_per)
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+    total_bytes = n_slots * (in_per + out_per)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"traffic_decode_r{rank}.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            traffic = json.load(fh).get("hbm_bytes_per_launch")
+    line = {
+        "metric": "bulk decode GB/s (packed 9-bit indices -> dense bf16 A/B), 342 FLUX linears",
+        "value": round(total_bytes / (ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"bulk decode of a {n_slots}-adapter packed bank (342 FLUX.1-dev linears, rank "
+                               f"{rank}) to dense bf16, {chunk} adapters per launch into a reused buffer",
+                   "rank": rank, "bank_slots": n_slots, "bank_GB": round(n_slots * in_per / 1e9, 2),
+                   "adapters_per_launch": chunk, "out_MB_per_adapter": round(out_per / 1e6, 2)},
+        "adapters_per_s": round(n_slots / (ms * 1e-3), 1),
+        "roofline": {"kernel": "decode_kernel (lithe_decode)", "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": launch_bytes,
+                     "mean_launch_ms": round(launch_ms, 4)},
+        "copy_GBps": round(copy_bandwidth_gbps(), 1),
+        "cpu_baseline": None if args.no_cpu else cpu_decode_baseline(layout),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="flux342", choices=["flux342", "ffn", "hb"])
+    ap.add_argument("--config", default="flux342", choices=["flux342", "ffn", "hb", "decode"])
+    ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--slots", type=int, default=None, help="bank size (default: the configuration's)")
@@ -249,6 +348,9 @@ def main():
         sys.exit(2)
     from lithe_amd.kernels import _hip
     _hip.load()
+    if args.config == "decode":
+        run_decode(args)
+        return
     rng = np.random.default_rng(1234)
     if args.config == "flux342":
         mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
