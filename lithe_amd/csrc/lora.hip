@@ -72,7 +72,7 @@ struct LoraArgs {
     int64_t n_batch, seq, d_in, d_out, rows;
     int32_t rank, G, n_rg, n_route, MR;
     int32_t tiles_s, ks, pb, arow, region, red_off, stage_off;
-    int32_t tiles_e, subs_e, BO, vec_y, nblk_max;
+    int32_t tiles_e, subs_e, BO, vec_y, nblk_max, estage_off;
     int32_t accumulate;
     float out_scale;
     const int32_t *r_slot;
@@ -116,13 +116,10 @@ __device__ __forceinline__ V stream_load(const V *p) {
     if constexpr (FORCE_NT || LITHE_STREAM_NT) return __builtin_nontemporal_load(p);
     else return *p;
 }
-template <typename V>
+template <typename V, bool FORCE_NT = false>
 __device__ __forceinline__ void stream_store(V *p, const V &v) {
-#if LITHE_STREAM_NT
-    __builtin_nontemporal_store(v, p);
-#else
-    *p = v;
-#endif
+    if constexpr (FORCE_NT || LITHE_STREAM_NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
 }
 
 template <typename XT>
@@ -545,6 +542,8 @@ template <> struct Y8<float> {
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
 __device__ __forceinline__ void expand_body(const LoraArgs &a) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
+    // bf16 y with output tiles of whole lines: the whole-line y path (line_subtile below)
+    constexpr bool LINE = sizeof(YT) == 2 && BOM % 64 == 0;
     typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -766,6 +765,65 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
     // ---- sub-tiles: 16 tokens per wave each. Every load of a sub-tile is issued up front
     // (rows and columns clamped in range); waves of other workgroups hide the latency.
     const int64_t omax = a.d_out - 8;
+
+    // Whole-line y path (bf16 y). The y tile of a wave (16 tokens x BOM outputs) moves in
+    // loads and stores that each cover whole 128-byte lines: access j gives lane L token
+    // 8 (j & 1) + L / 8 and outputs 64 (j >> 1) + 8 (L % 8) .. + 7, with the non-temporal hint
+    // (measured: +5 % read-modify-write bandwidth; split-line accesses lose with it). The
+    // delta d = round_y(round_y(acc) * s) is finished in the MFMA layout (lane: token r16,
+    // outputs 32 p + 8 gq ..) and exchanged through a per-wave LDS tile: 16-byte unit
+    // (token t, chunk q) at (BOM / 8) t + (q ^ swz(t)), conflict-free for both sides at BOM >= 128.
+    constexpr int NJ = BOM / 32;
+    auto line_subtile = [&](int sub, const Frag *mf) __attribute__((always_inline)) {
+        __bf16 *stg = reinterpret_cast<__bf16 *>(smem + a.estage_off) + wave * 16 * BOM;
+        constexpr int RU = BOM / 8;    // 16-byte units per token row of the tile
+        auto unit = [&](int t, int q) __attribute__((always_inline)) {
+            const int swz = ((t & 7) | ((((t >> 3) ^ t) & 1) << 3)) & (RU - 1);
+            return stg + (RU * t + (q ^ swz)) * 8;
+        };
+        const int lr = lane >> 3, lc = lane & 7;
+        int64_t lrow[2];
+        bool lval[2];
+#pragma unroll
+        for (int eta = 0; eta < 2; ++eta) {
+            const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + 8 * eta + lr;
+            lval[eta] = m < a.seq;
+            lrow[eta] = (b * a.seq + (lval[eta] ? m : a.seq - 1)) * a.d_out;
+        }
+        __bf16 *yb = static_cast<__bf16 *>(a.y);
+        bf16x8 yv[NJ];
+        if constexpr (ACC) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                yv[j] = stream_load<bf16x8, true>(reinterpret_cast<const bf16x8 *>(
+                    yb + lrow[j & 1] + std::min<int64_t>(obase + 64 * (j >> 1) + 8 * lc, omax)));
+        }
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            if (p >= np) break;
+            float vals[8];
+            compute(mf, p, vals);
+            bf16x8 d;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d[e] = (__bf16)(DT<YT>::round(vals[e]) * s_b);
+            *reinterpret_cast<bf16x8 *>(unit(r16, 4 * p + gq)) = d;
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int t = 8 * (j & 1) + lr, q = 8 * (j >> 1) + lc;
+            const bf16x8 d = *reinterpret_cast<const bf16x8 *>(unit(t, q));
+            const int64_t o8 = obase + 8 * q;
+            bf16x8 out;
+            if constexpr (ACC) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) out[e] = (__bf16)((float)yv[j][e] + (float)d[e]);
+            } else {
+                out = d;
+            }
+            if (lval[j & 1] && 8 * q < a.BO && o8 < a.d_out)
+                stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + lrow[j & 1] + o8), out);
+        }
+    };
     for (int sub = 0; sub < a.subs_e; ++sub) {
         // keeps the B fragment reads inside the loop (read from LDS per use, not held in registers)
         asm volatile("" ::: "memory");
@@ -779,6 +837,12 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
             else mf[g] = *reinterpret_cast<const f32x4 *>(src);
         }
         YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
+        if constexpr (LINE) {
+            if (a.vec_y) {
+                line_subtile(sub, mf);
+                continue;
+            }
+        }
         if (a.vec_y) {
             Y8<YT> yv[NP];
             if constexpr (ACC) {
@@ -839,14 +903,14 @@ struct Plan {
     int G, n_rg, GM, MR;
     int tiles_s, ks, pb, arow, region, red_off, stage_off;
     size_t lds_s, lds_e;
-    int tiles_e, subs_e, BO, BOM, U, nblk_max;
+    int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off;
     int64_t off_mid, total;
 };
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
 Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int rank, int n_route, int xbytes,
-               bool dense) {
+               bool dense, int ybytes = 2) {
     Plan p{};
     p.n_rg = (rank + 15) / 16;
     p.G = p.n_rg * n_route;
@@ -901,6 +965,9 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // B periods of one output tile: the blocks covering outputs [obase, obase + BO) of a route
     p.nblk_max = (int)(((int64_t)p.BO * rank + kBlock - 1) / kBlock + 1);
     p.lds_e = kHead + (dense ? (size_t)n_route * p.BO * rank * xbytes : (size_t)n_route * p.nblk_max * 16 * xbytes);
+    // whole-line y path (bf16 y, output tiles of whole lines): a 16 x BOM bf16 tile per wave
+    p.estage_off = (int)((p.lds_e + 15) & ~size_t(15));
+    if (ybytes == 2 && p.BOM % 64 == 0) p.lds_e = p.estage_off + (size_t)kWaves * 16 * p.BOM * 2;
 
     // workspace: [error word | mid]
     p.off_mid = 256;
@@ -1019,7 +1086,8 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
         return LITHE_ERR_DTYPE;
     }
 
-    const Plan p = make_plan(n_batch, seq, d_in, d_out, rank, routes->n_route, xbytes, f->kind == LITHE_FACTOR_DENSE);
+    const Plan p = make_plan(n_batch, seq, d_in, d_out, rank, routes->n_route, xbytes, f->kind == LITHE_FACTOR_DENSE,
+                             ybytes);
     if (workspace_bytes < p.total) return LITHE_ERR_WORKSPACE;
 
     char *ws = static_cast<char *>(workspace);
@@ -1048,6 +1116,7 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     a.subs_e = p.subs_e;
     a.BO = p.BO;
     a.nblk_max = p.nblk_max;
+    a.estage_off = p.estage_off;
     a.vec_y = (d_out % 8 == 0) && (((uintptr_t)y & 15u) == 0);
     a.accumulate = accumulate ? 1 : 0;
     a.out_scale = out_scale;

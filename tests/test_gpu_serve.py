@@ -152,3 +152,24 @@ def test_lithe_linear_inference():
         got = to_np(model(x.cuda()))
     want = odelta.lithe_linear(to_np(x), base_out, a_hat, b_hat, 0.5, "bf16")
     assert rel(got, want) < 2e-3
+
+
+@pytest.mark.parametrize("n_routes,rank,d_out", [(2, 16, 200), (6, 16, 200), (8, 16, 328), (2, 32, 264), (5, 8, 96)])
+def test_serve_bf16_rank_group_tiles(n_routes, rank, d_out):
+    """bf16 mixtures over 2..8 rank groups: every output-tile width of the expand (256, 128
+    and 64 outputs), partial last tiles, a ragged token count and a sample with one route
+    entry fewer than the others (an empty rank group)."""
+    rng = np.random.default_rng(n_routes * 100 + rank)
+    n_ad = n_routes + 1
+    routes = []
+    for i in range(3):
+        k = n_routes if i != 1 else n_routes - 1
+        ids = rng.choice(n_ad, k, replace=False)
+        w = rng.uniform(0.2, 1.0, k)
+        w = w / w.sum()
+        routes.append([(int(a), float(v)) for a, v in zip(ids, w)])
+    x = torch.randn(3, 37, 192, generator=torch.Generator().manual_seed(n_routes)).bfloat16()
+    y, want, _ = _serve_case(192, d_out, rank, n_ad, routes, x, alpha=2.0 * rank, dtype=torch.bfloat16)
+    err = rel(y, want)
+    print(f"serve bf16 routes={n_routes} rank={rank} d_out={d_out}: rel vs oracle {err:.2e}")
+    assert err < 2e-3
