@@ -7,6 +7,8 @@
 // per-element cost is a quarter of a direct decode.
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "lithe_common.h"
 
 namespace lithe {
@@ -112,6 +114,72 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
         for (int j = 0; j < 4; ++j) {
             *reinterpret_cast<f32x4 *>(out + 16 * j) = lo;
             *reinterpret_cast<f32x4 *>(out + 16 * j + 4) = hi;
+        }
+    }
+}
+
+// Packed 3-level fast path of the bulk decode (the resident bank of the twin codebook). Each
+// thread owns ITER half-blocks of one selected slot, spaced kThreads apart, and issues the
+// index loads of all of them before decoding the first, so a wave keeps ITER round trips in
+// flight instead of one; the workgroup count drops ITER-fold. Output order and values are
+// those of decode_kernel.
+constexpr int kDecodeIter = 8;
+template <typename OutT>
+__global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) {
+    __shared__ float lut[2 * kMaxLevels * 10];
+    if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
+
+    const int sel = blockIdx.y;
+    const int64_t slot = a.slots ? a.slots[sel] : 0;
+    const bool bad = slot < 0 || slot >= a.src.n_slots;
+    const int64_t halves = a.n_blocks * 2;
+    const int64_t h0 = (int64_t)blockIdx.x * (kThreads * kDecodeIter) + threadIdx.x;
+    OutT *out = static_cast<OutT *>(a.out) + (int64_t)sel * a.out_sel_stride;
+
+    int64_t blk[kDecodeIter], sl[kDecodeIter];
+    RawIdx raw[kDecodeIter];
+    int8_t side[kDecodeIter];
+#pragma unroll
+    for (int i = 0; i < kDecodeIter; ++i) {
+        const int64_t hf = std::min(h0 + (int64_t)i * kThreads, halves - 1);   // clamped: loads stay in range
+        blk[i] = hf >> 1;
+        sl[i] = bad ? 0 : slot;
+    }
+    load_raw<kDecodeIter, true, 3>(a.src, sl, blk, raw);
+#pragma unroll
+    for (int i = 0; i < kDecodeIter; ++i) side[i] = a.sides ? a.sides[blk[i]] : 0;
+    __syncthreads();    // value tables staged
+    if (bad && threadIdx.x == 0 && blockIdx.x == 0) record_error(a.err, kErrSlot);
+
+#pragma unroll
+    for (int i = 0; i < kDecodeIter; ++i) {
+        const int64_t hf = h0 + (int64_t)i * kThreads;
+        if (hf >= halves) break;
+        const int h = (int)(hf & 1);
+        uint32_t k[kMaxLevels];
+        extract_indices<true, 3>(a.src, blk[i], raw[i], k);
+        const float *tab = lut + (int)side[i] * kMaxLevels * 10;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t m = h ? sign_mask(8 + e) : sign_mask(e);
+            v[e] = bad ? 0.0f : decode_value<3>(tab, 3, k, m);
+        }
+        OutT *o = out + blk[i] * kBlock + 8 * h;
+        if constexpr (sizeof(OutT) == 2) {
+            bf16x8 pk;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pk[e] = (__bf16)v[e];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<bf16x8 *>(o + 16 * j) = pk;
+        } else {
+            f32x4 lo = {v[0], v[1], v[2], v[3]};
+            f32x4 hi = {v[4], v[5], v[6], v[7]};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                *reinterpret_cast<f32x4 *>(o + 16 * j) = lo;
+                *reinterpret_cast<f32x4 *>(o + 16 * j + 4) = hi;
+            }
         }
     }
 }
@@ -225,6 +293,14 @@ extern "C" int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots
     a.out_sel_stride = out_sel_stride;
     a.err = err_flag;
     const int64_t halves = n_blocks * 2;
+    if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3) {
+        dim3 grid((unsigned)((halves + kThreads * kDecodeIter - 1) / (kThreads * kDecodeIter)), (unsigned)n_sel);
+        if (out_dtype == LITHE_DT_BF16)
+            hipLaunchKernelGGL(decode_packed3_kernel<__bf16>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(decode_packed3_kernel<float>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+        return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+    }
     dim3 grid((unsigned)((halves + kThreads - 1) / kThreads), (unsigned)n_sel);
     if (out_dtype == LITHE_DT_BF16)
         hipLaunchKernelGGL(decode_kernel<__bf16>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);

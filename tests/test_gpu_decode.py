@@ -127,3 +127,37 @@ def test_bank_random_fill_fields_in_range():
     n = bank.layout.num_indices
     fields = opk.unpack(w[3], bank.layout.num_words * 7)
     assert (fields[n:] == 0).all() and fields[:n].max() <= 511
+
+
+def test_decode_bad_slot_zero_fills_and_flags():
+    """lithe_decode through the C ABI: a slot id outside the bank decodes to zeros and sets
+    bit 1 of the error word; the valid selections beside it stay bit-exact."""
+    import ctypes
+
+    from lithe_amd.kernels import _delta, _hip
+    ads = [random_adapter(SMALL, rank=16, seed=s) for s in range(3)]
+    bank, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bank.add(w)
+    lay = bank.layout
+    sel = [2, 7, -1, 0]
+    out = torch.full((len(sel), lay.total_blocks, 64), 3.0, dtype=torch.bfloat16, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    src = _delta.packed_source(bank.words, lay.num_levels, 0)
+    lut_a = _hip.lut_from_pools(bank.pool_a, torch.float32)
+    lut_b = _hip.lut_from_pools(bank.pool_b, torch.float32)
+    slots = torch.tensor(sel, dtype=torch.int32, device="cuda")
+    rc = _hip.load().lithe_decode(ctypes.byref(src), _hip.ptr(slots), len(sel), lay.total_blocks,
+                                  _hip.ptr(lay.sides_on("cuda")), ctypes.byref(lut_a), ctypes.byref(lut_b),
+                                  _hip.ptr(out), _hip.dtype_code(out.dtype), lay.total_blocks * 64, _hip.ptr(err),
+                                  _hip.stream_of(out.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    for i, s in enumerate(sel):
+        got = out[i].view(torch.int16).cpu().numpy().view(np.uint16)
+        if 0 <= s < 3:
+            _, bits, _ = _oracle_decode_bits(ads[s])
+            assert np.array_equal(got, bits), i
+        else:
+            assert not got.any(), i      # bf16 +0.0 everywhere
