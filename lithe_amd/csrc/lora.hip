@@ -54,7 +54,7 @@ constexpr int kMaxGroups = 8;
 constexpr int kLutFloats = kMaxLevels * 10;
 constexpr int kHead = 256;
 static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
-constexpr int kFillBatch = 2;     // fill items per thread whose loads are issued together
+constexpr int kFillBatch = 3;     // fill items per thread whose loads are issued together
 constexpr int kShrinkU = 4;       // k-steps per shrink load batch (even: loads move step pairs)
 
 // Factor sources: SRC_PACKED is SRC_INDEXED with both index streams PACKED9 with 3 levels (the
@@ -932,13 +932,17 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.tiles_s = (int)std::max<int64_t>(1, (seq + 16 * tgw - 1) / (16 * tgw));
     // Ring of two LDS regions, each holding the GM*16 factor rows of one K piece of pb blocks:
     // periods (16 values per block; the plan keeps a piece's items within one fill batch) or
-    // dense rows (64 values per block).
+    // dense rows (64 values per block). Every piece boundary is a workgroup barrier, so pieces
+    // are as long as the fill batch allows; a factor that fits one piece gets one region.
     const int pad = 16 / xbytes;
     if (dense) {
         p.pb = std::max(1, 4 / p.GM);
         p.arow = p.pb * kBlock + pad;
     } else {
-        p.pb = std::max(1, std::min(16, kFillBatch * kThreads / (p.GM * 16)));
+        // Few token groups (K split over 4 waves): one long piece (fewer barriers) wins; with
+        // whole-K waves the LDS of a long piece costs a workgroup of occupancy, and 16 wins
+        // (measured over the FLUX shapes).
+        p.pb = std::max(1, std::min(ks >= 4 ? 48 : 16, kFillBatch * kThreads / (p.GM * 16)));
         p.arow = p.pb * 16 + pad;
     }
     if (getenv("LITHE_SHRINK_PB") && !dense) {
@@ -946,7 +950,8 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
         p.arow = p.pb * 16 + pad;
     }
     p.region = p.GM * 16 * p.arow;
-    p.red_off = kHead + 2 * p.region * xbytes;
+    const int64_t npiece = (d_in / kBlock + p.pb - 1) / p.pb;
+    p.red_off = kHead + (npiece > 1 ? 2 : 1) * p.region * xbytes;
     p.stage_off = p.red_off + (ks > 1 ? kWaves * p.GM * 64 * 16 : 0);
     p.lds_s = p.stage_off + (size_t)kWaves * kShrinkU * 1024;
 
@@ -958,7 +963,9 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);
     const int64_t o_tiles = (d_out + p.BO - 1) / p.BO;
     const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
-    int subs = base_wgs >= 4 * 256 ? 2 : 1;    // 2 sub-tiles of 64 tokens: measured best at every FLUX shape
+    // 2 sub-tiles of 64 tokens per workgroup only for mid-sized grids (the 512-token, 3072-output
+    // FLUX modules); everywhere else one sub-tile (more, shorter workgroups) measured faster.
+    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256) ? 2 : 1;
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
