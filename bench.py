@@ -10,7 +10,7 @@ inside the kernels. Inputs are synthetic (x, y ~ N(0, 1); uniformly random
 9-bit fields) and already resident in HBM; x / y buffers rotate so the 256 MB
 Infinity Cache cannot serve a module from a previous module's data.
 
-    python bench.py [--steps K] [--warmup W] [--config flux342|ffn|hb|decode] [--rank 16|64]
+    python bench.py [--steps K] [--warmup W] [--config flux342|ffn|hb|decode|ingest] [--rank 16|64]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -326,12 +326,132 @@ def run_decode(args):
     print(json.dumps(line), flush=True)
 
 
+def run_ingest(args):
+    """Cold swap into a resident 10,000-slot bank: adapter file on disk -> packed slot ready to serve."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from lithe_amd import fileio
+    from lithe_amd.kernels import PackedBank, PackedLayout, _hip
+    from oracle import packing as opk
+    dev = torch.device("cuda:0")
+    mods = flux_modules(4096, 512)
+    modules = [{"name": n, "shape_a": [RANK, di], "shape_b": [do, RANK]} for n, di, do, _ in mods]
+    layout = PackedLayout.from_modules(modules, num_levels=3, block_size=64, scaling=1.0)
+    n_slots = args.slots or 10_000
+    bank = PackedBank(layout, dev, capacity=n_slots)
+    bank.fill_random(n_slots, generator=torch.Generator(device=dev).manual_seed(0))
+    rng = np.random.default_rng(0)
+    n_files = 4
+    tmp = tempfile.mkdtemp(prefix="lithe_ingest_")
+    lithe_paths, blob_paths, streams = [], [], []
+    for i in range(n_files):
+        idx = {m["name"]: {"A": rng.integers(0, 512, (3, opk.num_blocks(m["shape_a"]))).astype(np.uint16),
+                           "B": rng.integers(0, 512, (3, opk.num_blocks(m["shape_b"]))).astype(np.uint16)}
+               for m in modules}
+        ad = fileio.LitheAdapter(modules=modules, indices=idx, rank=RANK, alpha=float(RANK))
+        p = os.path.join(tmp, f"a{i}.lithe")
+        fileio.save_lithe(p, ad)
+        lithe_paths.append(p)
+        b = os.path.join(tmp, f"a{i}.int16.bin")
+        opk.stream_order(ad, opk.layout_of(ad)).astype(np.int16).tofile(b)
+        blob_paths.append(b)
+        streams.append(np.frombuffer(ad.raw_stream(), "<u2"))
+    file_mb = sum(os.path.getsize(p) for p in lithe_paths) / n_files / 1e6
+
+    def timed(fn, n):
+        for i in range(2):
+            fn(i)
+        torch.cuda.synchronize()
+        ts = []
+        for i in range(n):
+            t0 = time.perf_counter()
+            fn(i)
+            torch.cuda.synchronize()
+            ts.append((time.perf_counter() - t0) * 1e3)
+        ts.sort()
+        return {"mean_ms": round(sum(ts) / len(ts), 4), "p50_ms": round(ts[len(ts) // 2], 4),
+                "p99_ms": round(ts[min(len(ts) - 1, int(0.99 * len(ts)))], 4)}
+
+    slot = n_slots - 1
+    n = max(8, args.steps)
+    res = {
+        "lithe_file": timed(lambda i: bank.load_lithe(lithe_paths[i % n_files], slot=slot), n),
+        "lithe_file_noverify": timed(lambda i: bank.load_lithe(lithe_paths[i % n_files], slot=slot, verify=False), n),
+        "raw_blob": timed(lambda i: bank.load_blob(blob_paths[i % n_files], slot=slot), n),
+        "stream_device_pack": timed(lambda i: bank.load_stream(streams[i % n_files], slot=slot), n),
+        "stream_host_pack": timed(lambda i: bank.load_stream(streams[i % n_files], slot=slot, on_device=False), n),
+        "decode_on_swap": timed(lambda i: bank.decode(slot), n),
+    }
+    # the device reorder + pack kernel alone, HIP events on the launch stream
+    stream_t = torch.from_numpy(streams[0].view(np.int16).copy()).to(dev)
+    table = layout.ingest_table().to(dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    lib = _hip.load()
+    row = bank.words[slot]
+    cs = torch.cuda.current_stream()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        lib.lithe_ingest(_hip.ptr(stream_t), stream_t.numel(), 3, table.shape[0], _hip.ptr(table), _hip.ptr(row),
+                         layout.num_words, _hip.ptr(err), _hip.stream_of(dev))
+    s.record(cs)
+    reps = 50
+    for _ in range(reps):
+        lib.lithe_ingest(_hip.ptr(stream_t), stream_t.numel(), 3, table.shape[0], _hip.ptr(table), _hip.ptr(row),
+                         layout.num_words, _hip.ptr(err), _hip.stream_of(dev))
+    e.record(cs)
+    torch.cuda.synchronize()
+    k_ms = s.elapsed_time(e) / reps
+    k_bytes = layout.num_indices * 2 + layout.num_words * 8
+    assert int(err.item()) == 0
+    cpu = None
+    if not args.no_cpu:
+        # the same raw-blob path in the oracle: read the residency-ordered int16 blob, 9-bit pack
+        t0, k = time.perf_counter(), 0
+        while k < 20 or time.perf_counter() - t0 < 10.0:
+            opk.pack(np.fromfile(blob_paths[k % n_files], dtype=np.int16))
+            k += 1
+        per = (time.perf_counter() - t0) / k
+        t1, kl = time.perf_counter(), 0
+        while kl < 2 or time.perf_counter() - t1 < 5.0:
+            _, st = fileio.read_stream(lithe_paths[kl % n_files])
+            opk.pack(opk.residency_from_file_stream(st, modules, 3))
+            kl += 1
+        res["oracle_lithe_file_ms"] = round((time.perf_counter() - t1) / kl * 1e3, 2)
+        cpu = {"value": round(per * 1e3, 3), "unit": "ms per swap", "cores": 1, "kind": "port",
+               "sample": f"oracle (numpy) read of the residency-ordered int16 blob + 9-bit pack, {k} blobs of the "
+                         f"342-linear layout (the .lithe path, LZMA included: {kl} files, in paths)"}
+    for p in lithe_paths + blob_paths:
+        os.remove(p)
+    os.rmdir(tmp)
+    line = {
+        "metric": "cold-swap latency: adapter index blob on disk -> packed bank slot ready to serve "
+                  "(342 FLUX linears, rank 16)",
+        "value": res["raw_blob"]["mean_ms"], "unit": "ms", "n_gpus": 1, "steps": n, "warmup": 2,
+        "ms_per_step": res["raw_blob"]["mean_ms"], "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u16->u64", "data": "synthetic",
+        "config": {"workload": f"cold swap of one adapter ({layout.num_indices} indices: residency-ordered int16 "
+                               f"blob of {layout.num_indices * 2 / 1e6:.2f} MB, or a .lithe file of {file_mb:.2f} "
+                               f"MB) into slot {slot} of a resident {n_slots}-slot packed bank",
+                   "bank_slots": n_slots, "slot_MB": round(layout.num_words * 8 / 1e6, 3)},
+        "paths": res,
+        "roofline": {"kernel": "ingest_kernel (lithe_ingest)", "bound": "hbm",
+                     "achieved": round(k_bytes / (k_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": k_bytes, "mean_launch_ms": round(k_ms, 5)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="flux342", choices=["flux342", "ffn", "hb", "decode"])
+    ap.add_argument("--config", default="flux342", choices=["flux342", "ffn", "hb", "decode", "ingest"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -352,6 +472,9 @@ def main():
     _hip.load()
     if args.config == "decode":
         run_decode(args)
+        return
+    if args.config == "ingest":
+        run_ingest(args)
         return
     rng = np.random.default_rng(1234)
     if args.config == "flux342":

@@ -89,6 +89,32 @@ int32_t lithe_pack9(const void *idx, int32_t idx_dtype, int64_t n, uint64_t *wor
  * Replaces unpack_indices, lithe/kernels/packed.py:55-60. */
 int32_t lithe_unpack9(const uint64_t *words, int64_t n, void *out, int32_t out_dtype, void *stream);
 
+/* ---------------------------------------------------------------- ingest (.lithe stream -> bank slot) */
+/* The .lithe index stream (lithe/fileio.py:1-13) holds the A matrices of every module in header
+ * order, then the B matrices, each as its (L, n_blocks) matrix in row-major order. The residency
+ * order of a bank slot is (block, level)-major with each module's A blocks followed by its B
+ * blocks (lithe/kernels/packed.py:125-133). A layout's segment table has one row of three int64
+ * per factor, in residency order (module m: A = row 2m, B = row 2m + 1): first residency block,
+ * block count, first element of the factor in the stream.
+ * Replaces the module bookkeeping of load_lithe (lithe/fileio.py:136-150) and PackedLayout
+ * (lithe/kernels/packed.py:100-117). */
+int32_t lithe_ingest_table(int32_t n_modules, const int64_t *blocks_a, const int64_t *blocks_b,
+                           int32_t num_levels, int64_t *table);
+
+/* Host: reorder n_stream uint16 stream indices into the residency order and pack them 7 per word
+ * (words[n_words], zero-padded). LITHE_ERR_RANGE (nothing written) if any index > 511,
+ * LITHE_ERR_SHAPE if the table does not describe exactly n_stream indices.
+ * Replaces flat_indices + pack_indices over a loaded adapter (lithe/kernels/packed.py:38-52, 125-143). */
+int32_t lithe_ingest_host(const uint16_t *stream, int64_t n_stream, int32_t num_levels, int32_t n_segments,
+                          const int64_t *table, uint64_t *words, int64_t n_words);
+
+/* Device: the same from a device stream and a device copy of the table, written straight into
+ * `words` (e.g. a bank slot). *err_flag (device int32, nullable) gets bit 1 for an index > 511
+ * (packed as 0) and bit 2 for a table position outside the stream (read as index 0). */
+int32_t lithe_ingest(const uint16_t *stream, int64_t n_stream, int32_t num_levels, int32_t n_segments,
+                     const int64_t *table, uint64_t *words, int64_t n_words, int32_t *err_flag,
+                     void *stream_hip);
+
 /* ---------------------------------------------------------------- bulk decode */
 /* Decode n_blocks 64-value blocks of each selected slot to dense values:
  *   out[s][blk][t] = sum_l lut_side(blk).value[l][popcount((k_l ^ m_t) & 511)]   (fp32, l in order)

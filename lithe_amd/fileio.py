@@ -111,7 +111,13 @@ def read_header(path) -> Dict[str, Any]:
     return _read(path)[0]
 
 
-def load_lithe(path, verify: bool = True) -> LitheAdapter:
+def read_stream(path, verify: bool = True):
+    """(header, index stream) of a ``.lithe`` file without splitting it per module.
+
+    The stream is the file's little-endian uint16 index stream (A matrices of every module,
+    then the B matrices), read-only. With ``verify`` the payload and codebook SHA-256 are
+    checked as ``load_lithe`` does (``lithe/fileio.py:124-129``).
+    """
     header, body = _read(path)
     raw = lzma.decompress(body)
     book = header["codebook"]
@@ -120,7 +126,12 @@ def load_lithe(path, verify: bool = True) -> LitheAdapter:
             raise ValueError(f"{path}: payload checksum mismatch")
         if book["sha256"] != cb.codebook_sha256(book["block_size"], book["n_bits"]):
             raise ValueError(f"{path}: codebook hash mismatch")
-    stream = np.frombuffer(raw, dtype="<u2")
+    return header, np.frombuffer(raw, dtype="<u2")
+
+
+def load_lithe(path, verify: bool = True) -> LitheAdapter:
+    header, stream = read_stream(path, verify)
+    book = header["codebook"]
     L, bs = int(book["num_levels"]), int(book["block_size"])
     modules = header["modules"]
 

@@ -71,6 +71,9 @@ SIGNATURES = {
                           ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _F32, _P,
                           _P, _I64, _P], _I32),
     "lithe_workspace_errors": ([_P, _P, _I32, _P], _I32),
+    "lithe_ingest_table": ([_I32, _P, _P, _I32, _P], _I32),
+    "lithe_ingest_host": ([_P, _I64, _I32, _I32, _P, _P, _I64], _I32),
+    "lithe_ingest": ([_P, _I64, _I32, _I32, _P, _P, _I64, _P, _P], _I32),
 }
 
 _lib = None
@@ -90,7 +93,11 @@ def load(path: str = LIB_PATH):
                 raise RuntimeError(_lib_err)
             lib = ctypes.CDLL(path)
             for name, (args, res) in SIGNATURES.items():
-                fn = getattr(lib, name)
+                try:
+                    fn = getattr(lib, name)
+                except AttributeError:
+                    _lib_err = f"{path} is stale: it does not export {name} (rebuild it)"
+                    raise RuntimeError(_lib_err) from None
                 fn.argtypes = args
                 fn.restype = res
             _lib = lib

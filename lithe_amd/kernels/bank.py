@@ -8,8 +8,10 @@ can address every slot through one pointer, and a 10,000-slot bank of the
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from .. import codebook as cb
@@ -31,6 +33,9 @@ class PackedBank:
         # int64 storage (torch has more kernels for it); the bits are the uint64 words.
         self._words = torch.zeros((max(1, int(capacity)), layout.num_words), dtype=torch.int64, device=self.device)
         self.num_slots = 0
+        self._free: List[int] = []        # freed slot ids, ascending
+        self._stage = None                 # (pinned stream, device stream, error word, copy event)
+        self._tdev = None                  # device copy of the layout's ingest table
 
     # -------------------------------------------------------------- construction
     @classmethod
@@ -103,6 +108,141 @@ class PackedBank:
 
     def shrink_to(self, n: int) -> None:
         self.num_slots = min(self.num_slots, max(0, n))
+        self._free = [f for f in self._free if f < self.num_slots]
+
+    # -------------------------------------------------------------- slot allocation
+    def alloc(self) -> int:
+        """A slot id to load an adapter into: the lowest freed slot, else a new one at the end."""
+        if self._free:
+            return self._free.pop(0)
+        if self.num_slots == self._words.shape[0]:
+            self.reserve(max(16, 2 * self.num_slots))
+        self.num_slots += 1
+        return self.num_slots - 1
+
+    def free(self, slot: int) -> None:
+        """Return ``slot`` to the allocator. Its words stay until the slot is reloaded; routing a
+        sample to a freed slot is the caller's error, as indexing a dropped list entry is in the
+        reference's bank."""
+        if not 0 <= slot < self.num_slots:
+            raise IndexError(f"slot {slot} is not resident")
+        if slot in self._free:
+            raise ValueError(f"slot {slot} is already free")
+        self._free.append(slot)
+        self._free.sort()
+
+    @property
+    def num_free(self) -> int:
+        return len(self._free)
+
+    # -------------------------------------------------------------- ingest
+    def _target(self, slot: Optional[int]) -> int:
+        if slot is None:
+            return self.alloc()
+        if not 0 <= slot < self.num_slots:
+            raise IndexError(f"slot {slot} is not resident (bank has {self.num_slots})")
+        if slot in self._free:
+            self._free.remove(slot)
+        return slot
+
+    def _staging(self, n: int):
+        """Pinned host and device buffers for one uint16 index stream, reused across loads."""
+        st = self._stage
+        if st is None or st[0].numel() < n:
+            pin = torch.empty(n, dtype=torch.int16, pin_memory=True)
+            dev = torch.empty(n, dtype=torch.int16, device=self.device)
+            err = torch.zeros(1, dtype=torch.int32, device=self.device)
+            st = (pin, dev, err, torch.cuda.Event())
+            self._stage = st
+        return st
+
+    def load_stream(self, stream, slot: Optional[int] = None, on_device: bool = True) -> int:
+        """Load one adapter from its ``.lithe`` index stream (uint16: the A matrices of every
+        module, then the B matrices) into a slot; returns the slot id.
+
+        ``on_device``: the stream is copied to the GPU and reordered + packed there straight into
+        the slot (``lithe_ingest``); otherwise the host packer builds the words
+        (``lithe_ingest_host``) and they are copied into the slot. Values above 511 raise
+        ValueError before anything is written. Asynchronous on the current stream.
+        """
+        arr = np.ascontiguousarray(np.asarray(stream).reshape(-1)).view(np.uint16) if not isinstance(
+            stream, torch.Tensor) else stream.reshape(-1).contiguous().cpu().numpy().view(np.uint16)
+        lay = self.layout
+        if arr.size != lay.num_indices:
+            raise ValueError(f"stream holds {arr.size} indices, the layout needs {lay.num_indices}")
+        if arr.size and int(arr.max()) > 511:
+            raise ValueError("indices must be < 512 for 9-bit packing")
+        table = lay.ingest_table()
+        target = self._target(slot)
+        row = self._words[target]
+        lib = _hip.load()
+        if on_device:
+            pin, dev, err, ev = self._staging(arr.size)
+            ev.synchronize()                        # the previous load's copy has left the pinned buffer
+            pin[: arr.size].numpy()[:] = arr.view(np.int16)
+            dev[: arr.size].copy_(pin[: arr.size], non_blocking=True)
+            ev.record()
+            tdev = self._table_dev(table)
+            rc = lib.lithe_ingest(_hip.ptr(dev), arr.size, lay.num_levels, table.shape[0], _hip.ptr(tdev),
+                                  _hip.ptr(row), lay.num_words, _hip.ptr(err), _hip.stream_of(self.device))
+            _hip.check(rc, "lithe_ingest")
+        else:
+            words = np.empty(lay.num_words, np.uint64)
+            rc = lib.lithe_ingest_host(arr.ctypes.data_as(ctypes.c_void_p), arr.size, lay.num_levels, table.shape[0],
+                                       table.numpy().ctypes.data_as(ctypes.c_void_p),
+                                       words.ctypes.data_as(ctypes.c_void_p), lay.num_words)
+            _hip.check(rc, "lithe_ingest_host")
+            row.copy_(torch.from_numpy(words.view(np.int64)))
+        return target
+
+    def _table_dev(self, table: torch.Tensor) -> torch.Tensor:
+        if self._tdev is None:
+            self._tdev = table.to(self.device)
+        return self._tdev
+
+    def load_lithe(self, path, slot: Optional[int] = None, verify: bool = True, on_device: bool = True) -> int:
+        """Cold swap from a ``.lithe`` file (``lithe/fileio.py:119-152`` then ``pack_adapter``,
+        ``lithe/kernels/packed.py:136-143``): read and check the file, then ``load_stream``.
+        The file's modules, levels and block size must be the bank's layout."""
+        from ..fileio import read_stream
+        header, stream = read_stream(path, verify)
+        book = header["codebook"]
+        if not self.layout.matches_modules(header["modules"], int(book["num_levels"]), int(book["block_size"])):
+            raise ValueError(f"{path}: modules do not match the bank layout")
+        if int(book["n_bits"]) != 9:
+            raise ValueError(f"{path}: the bank holds 9-bit indices, the file has n_bits={book['n_bits']}")
+        return self.load_stream(stream, slot, on_device)
+
+    def load_blob(self, path, slot: Optional[int] = None) -> int:
+        """Cold swap from a raw index blob on disk: int16 indices already in the residency order
+        (``flat_indices(ad, layout).astype(np.int16).tofile(path)``, the blob of
+        ``serving/bench_hotswap.py:100-104``), packed on the GPU straight into the slot."""
+        lay = self.layout
+        arr = np.fromfile(path, dtype=np.int16)
+        if arr.size != lay.num_indices:
+            raise ValueError(f"{path}: {arr.size} indices, the layout needs {lay.num_indices}")
+        if arr.size and (int(arr.max()) > 511 or int(arr.min()) < 0):
+            raise ValueError("indices must be in [0, 511] for 9-bit packing")
+        target = self._target(slot)
+        pin, dev, err, ev = self._staging(arr.size)
+        ev.synchronize()
+        pin[: arr.size].numpy()[:] = arr
+        dev[: arr.size].copy_(pin[: arr.size], non_blocking=True)
+        ev.record()
+        rc = _hip.load().lithe_pack9(_hip.ptr(dev), _hip.DT_I16, arr.size, _hip.ptr(self._words[target]),
+                                     _hip.ptr(err), _hip.stream_of(self.device))
+        _hip.check(rc, "lithe_pack9")
+        return target
+
+    def ingest_errors(self, clear: bool = True) -> int:
+        """Error bits the device ingest recorded since the last clear (synchronises)."""
+        st = self._stage
+        if st is None:
+            return 0
+        v = int(st[2].item())
+        if clear and v:
+            st[2].zero_()
+        return v
 
     # -------------------------------------------------------------- decode
     def decode(self, slot: int) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:

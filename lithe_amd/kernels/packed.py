@@ -146,6 +146,27 @@ class PackedLayout:
         return cls(names=names, shapes_a=sa, shapes_b=sb, a_off=a_off, b_off=b_off, sides=sides,
                    num_levels=int(num_levels), block_size=int(block_size), scaling=float(scaling))
 
+    def ingest_table(self) -> torch.Tensor:
+        """(2 * n_modules, 3) int64 segment table of ``lithe_ingest``: per factor in residency
+        order, its first block, its block count and its first element in the ``.lithe`` stream."""
+        key = "ingest_table"
+        if key not in self._sides_dev:
+            ba = np.array([quant.num_blocks(s, self.block_size) for s in self.shapes_a], np.int64)
+            bb = np.array([quant.num_blocks(s, self.block_size) for s in self.shapes_b], np.int64)
+            table = np.zeros((2 * len(self.names), 3), np.int64)
+            rc = _hip.load().lithe_ingest_table(len(self.names), ba.ctypes.data_as(ctypes.c_void_p),
+                                                bb.ctypes.data_as(ctypes.c_void_p), self.num_levels,
+                                                table.ctypes.data_as(ctypes.c_void_p))
+            _hip.check(rc, "lithe_ingest_table")
+            self._sides_dev[key] = torch.from_numpy(table)
+        return self._sides_dev[key]
+
+    def matches_modules(self, modules: Sequence[Dict], num_levels: int, block_size: int) -> bool:
+        """True when ``modules`` ([{"name", "shape_a", "shape_b"}]) are this layout's, in order."""
+        return (num_levels == self.num_levels and block_size == self.block_size and len(modules) == len(self.names)
+                and all(m["name"] == n and tuple(m["shape_a"]) == a and tuple(m["shape_b"]) == b
+                        for m, n, a, b in zip(modules, self.names, self.shapes_a, self.shapes_b)))
+
     def matches(self, ad) -> bool:
         return (len(ad.modules) == len(self.names)
                 and all(m["name"] == n and tuple(m["shape_a"]) == a and tuple(m["shape_b"]) == b

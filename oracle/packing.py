@@ -138,6 +138,34 @@ def stream_order(ad, layout: Layout) -> np.ndarray:
     return np.concatenate(parts).astype(np.uint16)
 
 
+def split_file_stream(stream, modules, num_levels: int, block_size: int = 64):
+    """name -> {"A": (L, nA), "B": (L, nB)} from a ``.lithe`` index stream.
+
+    lithe/fileio.py:136-150: the stream holds the A matrices of every module in header order,
+    then the B matrices, each an (L, n_blocks) matrix in row-major order.
+    """
+    s = np.asarray(stream).reshape(-1)
+    out = {m["name"]: {} for m in modules}
+    cur = 0
+    for side, key in (("A", "shape_a"), ("B", "shape_b")):
+        for m in modules:
+            c = num_levels * num_blocks(m[key], block_size)
+            out[m["name"]][side] = s[cur:cur + c].reshape(num_levels, -1)
+            cur += c
+    if cur != s.size:
+        raise ValueError(f"stream length {s.size} does not match the modules ({cur})")
+    return out
+
+
+def residency_from_file_stream(stream, modules, num_levels: int, block_size: int = 64) -> np.ndarray:
+    """The ``.lithe`` stream reordered into the packed residency order (``split_file_stream``
+    then ``stream_order``: lithe/fileio.py:136-150, lithe/kernels/packed.py:125-133)."""
+    parts = split_file_stream(stream, modules, num_levels, block_size)
+    ad = {"modules": modules, "indices": parts, "block_size": block_size, "num_levels": num_levels,
+          "alpha": 1.0, "rank": 1}
+    return stream_order(ad, layout_of(ad))
+
+
 def pack_adapter(ad, layout: Layout = None):
     """(uint64 words, layout) for one adapter (lithe/kernels/packed.py:136-143)."""
     layout = layout or layout_of(ad)
