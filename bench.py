@@ -10,7 +10,7 @@ inside the kernels. Inputs are synthetic (x, y ~ N(0, 1); uniformly random
 9-bit fields) and already resident in HBM; x / y buffers rotate so the 256 MB
 Infinity Cache cannot serve a module from a previous module's data.
 
-    python bench.py [--steps K] [--warmup W] [--config flux342|ffn|hb|decode|ingest] [--rank 16|64]
+    python bench.py [--steps K] [--warmup W] [--config flux342|decoded|ffn|hb|decode|ingest] [--rank 16|64]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -57,12 +57,12 @@ def flux_modules(img_tokens: int, txt_tokens: int):
 class Workload:
     """Bank, buffers and prepared per-module calls of one configuration."""
 
-    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0):
+    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0, decoded=False):
         import numpy as np
         import torch
 
         from lithe_amd.kernels import PackedBank, PackedLayout
-        from lithe_amd.kernels.prepared import prepare_packed, shared_workspace, workspace_bytes
+        from lithe_amd.kernels.prepared import prepare_dense, prepare_packed, shared_workspace, workspace_bytes
 
         self.name, self.mods, self.batch = name, mods, batch
         dev = torch.device("cuda:0")
@@ -95,13 +95,33 @@ class Workload:
         need = max(workspace_bytes((batch, m, di), do, RANK, 1, torch.bfloat16) for _, di, do, m in mods)
         self.workspace = shared_workspace(dev, need)
         self.calls = []
+        uniq = sorted(set(np.asarray(assign).tolist()))
+        self.decode_ms = None
+        if decoded:
+            # decoded-mode serving: the routed slots decoded once (decode-on-swap) into stacked
+            # per-module bf16 factors, then every module reads dense factors
+            sel_of = {s: i for i, s in enumerate(uniq)}
+            self.sel = torch.tensor([sel_of[int(s)] for s in assign], dtype=torch.int32, device=dev)
+            self.bank.decode_stacked(uniq)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            self.factors = self.bank.decode_stacked(uniq)
+            torch.cuda.synchronize()
+            self.decode_ms = (time.perf_counter() - t0) * 1e3
         for n, di, do, m in mods:
             _, _, _, a_off, b_off = layout.module(n)
             x, y = buf(di, m), buf(do, m)
-            self.calls.append(prepare_packed(x, y, self.bank.words, a_off, b_off, 3, pools, self.assign, RANK,
-                                             1.0, self.workspace, accumulate=True))
+            if decoded:
+                a, b = self.factors[n]
+                self.calls.append(prepare_dense(x, y, a, b, self.sel, RANK, 1.0, self.workspace, accumulate=True))
+            else:
+                self.calls.append(prepare_packed(x, y, self.bank.words, a_off, b_off, 3, pools, self.assign, RANK,
+                                                 1.0, self.workspace, accumulate=True))
         self.tokens = batch * max(m for _, _, _, m in mods) if name != "ffn" else batch * mods[0][3]
-        self.index_bytes = len(set(np.asarray(assign).tolist())) * layout.num_words * 8
+        if decoded:   # dense factors of the routed adapters instead of their packed words
+            self.index_bytes = len(uniq) * sum(2 * RANK * (di + do) for _, di, do, _ in mods)
+        else:
+            self.index_bytes = len(uniq) * layout.num_words * 8
         self.alg_bytes = sum(c.algorithmic_bytes() for c in self.calls) + self.index_bytes
 
     def sweep(self, stream):
@@ -451,7 +471,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="flux342", choices=["flux342", "ffn", "hb", "decode", "ingest"])
+    ap.add_argument("--config", default="flux342", choices=["flux342", "decoded", "ffn", "hb", "decode", "ingest"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -477,11 +497,14 @@ def main():
         run_ingest(args)
         return
     rng = np.random.default_rng(1234)
-    if args.config == "flux342":
+    if args.config in ("flux342", "decoded"):
         mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
         assign = rng.choice(n_slots, batch, replace=False)
-        wl = Workload("flux342", mods, batch, n_slots, assign)
+        wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config == "decoded")
         workload = "FLUX.1-dev 342 linears, 1024^2: B=14 x 4608 tokens (4096 img + 512 txt), 10k-adapter packed bank"
+        if args.config == "decoded":
+            workload += (", decoded mode: the 14 routed adapters decoded once to stacked bf16 factors "
+                         "(decode-on-swap), modules read dense factors")
     elif args.config == "hb":
         mods, batch, n_slots = flux_modules(256, 512), 96, args.slots or 10_000
         ranks = np.arange(1, n_slots + 1, dtype=np.float64)
@@ -551,6 +574,8 @@ def main():
         "copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": cpu,
     }
+    if wl.decode_ms is not None:
+        line["decode_on_swap_ms"] = round(wl.decode_ms, 4)
     print(json.dumps(line), flush=True)
 
 

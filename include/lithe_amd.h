@@ -131,6 +131,21 @@ int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots, int32_t n
                      const lithe_lut *lut_b, void *out, int32_t out_dtype,
                      int64_t out_sel_stride, int32_t *err_flag, void *stream);
 
+/* Bulk decode into the stacked layout of decoded-mode serving: every factor of the layout gets
+ * its selections side by side, so module m's A is an (n_sel, rank, d_in) array and its B an
+ * (n_sel, d_out, rank) array, ready for LITHE_FACTOR_DENSE. table: device copy of the layout's
+ * segment table (lithe_ingest_table; rows in residency order, only the first two columns are
+ * read). Block blk of segment s (first block f, count n) of selection i is written at output
+ * block n_sel * f + i * n + (blk - f). err_flag bit 4: a table row maps a block outside the
+ * n_sel * n_blocks output blocks (nothing is written there). Otherwise as lithe_decode.
+ * Replaces decode_packed + split_decoded + the per-module torch.stack of
+ * PerSampleLoRALinear._build_stacked (lithe/kernels/packed.py:205-222, 260-269;
+ * lithe/kernels/layers.py:58-64). */
+int32_t lithe_decode_stacked(const lithe_index_src *src, const int32_t *slots, int32_t n_sel,
+                             int64_t n_blocks, int32_t n_segments, const int64_t *table,
+                             const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b,
+                             void *out, int32_t out_dtype, int32_t *err_flag, void *stream);
+
 /* ---------------------------------------------------------------- per-sample LoRA delta */
 /* Where the factors of the delta come from. */
 #define LITHE_FACTOR_INDEXED 1   /* decoded in-kernel from index sources + value tables */

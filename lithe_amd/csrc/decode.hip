@@ -69,7 +69,32 @@ struct DecodeArgs {
     int64_t n_blocks;
     int64_t out_sel_stride;
     int32_t *err;
+    // stacked output (decoded-mode serving): factor segments of the layout, rows of three int64
+    // (first block, block count, -); block blk of segment s and selection sel lands at block
+    // n_sel * first_s + sel * count_s + (blk - first_s) of the output. NULL: slot-major output.
+    const int64_t *seg;
+    int32_t n_seg;
+    int32_t n_sel;
 };
+
+// Output block of (selection sel, block blk) in the stacked layout; *s is the segment of a block
+// at or before blk on entry (0 works) and blk's segment on return.
+__device__ __forceinline__ int64_t stacked_block(const DecodeArgs &a, int32_t &s, int64_t blk, int sel) {
+    while (s + 1 < a.n_seg && blk >= a.seg[3 * (int64_t)s] + a.seg[3 * (int64_t)s + 1]) ++s;
+    const int64_t first = a.seg[3 * (int64_t)s], count = a.seg[3 * (int64_t)s + 1];
+    return (int64_t)a.n_sel * first + (int64_t)sel * count + (blk - first);
+}
+
+// Segment holding block blk (binary search over the first blocks).
+__device__ __forceinline__ int32_t find_seg(const DecodeArgs &a, int64_t blk) {
+    int32_t lo = 0, hi = a.n_seg;
+    while (hi - lo > 1) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (a.seg[3 * (int64_t)mid] <= blk) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
 
 template <typename OutT>
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
@@ -83,7 +108,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
     const int h = (int)(half & 1);
     const int sel = blockIdx.y;
     int64_t slot = a.slots ? a.slots[sel] : 0;
-    OutT *out = static_cast<OutT *>(a.out) + (int64_t)sel * a.out_sel_stride + block * kBlock + 8 * h;
+    int64_t ob = (int64_t)sel * (a.out_sel_stride / kBlock) + block;
+    if (a.seg) {
+        int32_t sg = find_seg(a, block);
+        ob = stacked_block(a, sg, block, sel);
+        if (ob < 0 || ob >= (int64_t)a.n_sel * a.n_blocks) {    // table inconsistent with n_blocks
+            record_error(a.err, kErrTable);
+            return;
+        }
+    }
+    OutT *out = static_cast<OutT *>(a.out) + ob * kBlock + 8 * h;
 
     float v[8];
     if (slot < 0 || slot >= a.src.n_slots) {
@@ -134,7 +168,8 @@ __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) 
     const bool bad = slot < 0 || slot >= a.src.n_slots;
     const int64_t halves = a.n_blocks * 2;
     const int64_t h0 = (int64_t)blockIdx.x * (kThreads * kDecodeIter) + threadIdx.x;
-    OutT *out = static_cast<OutT *>(a.out) + (int64_t)sel * a.out_sel_stride;
+    OutT *out = static_cast<OutT *>(a.out) + (a.seg ? 0 : (int64_t)sel * a.out_sel_stride);
+    int32_t sg = a.seg ? find_seg(a, std::min(h0, halves - 1) >> 1) : 0;
 
     int64_t blk[kDecodeIter], sl[kDecodeIter];
     RawIdx raw[kDecodeIter];
@@ -165,7 +200,12 @@ __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) 
             const uint32_t m = h ? sign_mask(8 + e) : sign_mask(e);
             v[e] = bad ? 0.0f : decode_value<3>(tab, 3, k, m);
         }
-        OutT *o = out + blk[i] * kBlock + 8 * h;
+        const int64_t ob = a.seg ? stacked_block(a, sg, blk[i], sel) : blk[i];
+        if (a.seg && (ob < 0 || ob >= (int64_t)a.n_sel * a.n_blocks)) {    // table inconsistent with n_blocks
+            record_error(a.err, kErrTable);
+            continue;
+        }
+        OutT *o = out + ob * kBlock + 8 * h;
         if constexpr (sizeof(OutT) == 2) {
             bf16x8 pk;
 #pragma unroll
@@ -261,9 +301,10 @@ extern "C" int32_t lithe_pack9(const void *idx, int32_t idx_dtype, int64_t n, ui
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
 }
 
-extern "C" int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots, int32_t n_sel, int64_t n_blocks,
-                                const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b, void *out,
-                                int32_t out_dtype, int64_t out_sel_stride, int32_t *err_flag, void *stream) {
+static int32_t decode_impl(const lithe_index_src *src, const int32_t *slots, int32_t n_sel, int64_t n_blocks,
+                           const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b, void *out,
+                           int32_t out_dtype, int64_t out_sel_stride, int32_t *err_flag, const int64_t *seg,
+                           int32_t n_seg, void *stream) {
     int32_t rc = check_src(src);
     if (rc) return rc;
     if (!src_covers(*src, n_blocks)) return LITHE_ERR_SHAPE;
@@ -292,6 +333,9 @@ extern "C" int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots
     a.n_blocks = n_blocks;
     a.out_sel_stride = out_sel_stride;
     a.err = err_flag;
+    a.seg = seg;
+    a.n_seg = n_seg;
+    a.n_sel = n_sel;
     const int64_t halves = n_blocks * 2;
     if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3) {
         dim3 grid((unsigned)((halves + kThreads * kDecodeIter - 1) / (kThreads * kDecodeIter)), (unsigned)n_sel);
@@ -307,4 +351,21 @@ extern "C" int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots
     else
         hipLaunchKernelGGL(decode_kernel<float>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+extern "C" int32_t lithe_decode(const lithe_index_src *src, const int32_t *slots, int32_t n_sel, int64_t n_blocks,
+                                const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b, void *out,
+                                int32_t out_dtype, int64_t out_sel_stride, int32_t *err_flag, void *stream) {
+    return decode_impl(src, slots, n_sel, n_blocks, sides, lut_a, lut_b, out, out_dtype, out_sel_stride, err_flag,
+                       nullptr, 0, stream);
+}
+
+extern "C" int32_t lithe_decode_stacked(const lithe_index_src *src, const int32_t *slots, int32_t n_sel,
+                                        int64_t n_blocks, int32_t n_segments, const int64_t *table,
+                                        const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b,
+                                        void *out, int32_t out_dtype, int32_t *err_flag, void *stream) {
+    if (!table) return LITHE_ERR_NULL;
+    if (n_segments < 1) return LITHE_ERR_SHAPE;
+    return decode_impl(src, slots, n_sel, n_blocks, sides, lut_a, lut_b, out, out_dtype, n_blocks * kBlock,
+                       err_flag, table, n_segments, stream);
 }

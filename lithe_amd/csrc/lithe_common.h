@@ -29,6 +29,7 @@ constexpr uint32_t kIndexMask = 0x1FFu;
 // Error bits written to the workspace error word.
 constexpr int32_t kErrSlot = 1;    // slot id outside [0, n_slots)
 constexpr int32_t kErrIndex = 2;   // level-major index outside [0, 511]
+constexpr int32_t kErrTable = 4;   // a segment table that maps a block outside the output
 
 // m_t for t in [0, 16): bit q set iff popcount(t & q) is even (q in [0, 9)).
 __host__ __device__ constexpr uint32_t sign_mask(uint32_t t) {

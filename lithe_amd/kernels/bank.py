@@ -16,7 +16,8 @@ import torch
 
 from .. import codebook as cb
 from . import _hip
-from .packed import PackedLayout, decode_packed_slots, pack_adapter, split_decoded
+from .packed import (PackedLayout, decode_packed_slots, decode_packed_stacked, pack_adapter, split_decoded,
+                     split_stacked)
 
 
 class PackedBank:
@@ -35,7 +36,6 @@ class PackedBank:
         self.num_slots = 0
         self._free: List[int] = []        # freed slot ids, ascending
         self._stage = None                 # (pinned stream, device stream, error word, copy event)
-        self._tdev = None                  # device copy of the layout's ingest table
 
     # -------------------------------------------------------------- construction
     @classmethod
@@ -182,7 +182,7 @@ class PackedBank:
             pin[: arr.size].numpy()[:] = arr.view(np.int16)
             dev[: arr.size].copy_(pin[: arr.size], non_blocking=True)
             ev.record()
-            tdev = self._table_dev(table)
+            tdev = lay.table_on(self.device)
             rc = lib.lithe_ingest(_hip.ptr(dev), arr.size, lay.num_levels, table.shape[0], _hip.ptr(tdev),
                                   _hip.ptr(row), lay.num_words, _hip.ptr(err), _hip.stream_of(self.device))
             _hip.check(rc, "lithe_ingest")
@@ -194,11 +194,6 @@ class PackedBank:
             _hip.check(rc, "lithe_ingest_host")
             row.copy_(torch.from_numpy(words.view(np.int64)))
         return target
-
-    def _table_dev(self, table: torch.Tensor) -> torch.Tensor:
-        if self._tdev is None:
-            self._tdev = table.to(self.device)
-        return self._tdev
 
     def load_lithe(self, path, slot: Optional[int] = None, verify: bool = True, on_device: bool = True) -> int:
         """Cold swap from a ``.lithe`` file (``lithe/fileio.py:119-152`` then ``pack_adapter``,
@@ -256,6 +251,17 @@ class PackedBank:
         if self.num_slots == 0:
             raise ValueError("bank is empty")
         return decode_packed_slots(self.words, slots, self.layout, self.pool_a, self.pool_b, out=out, dtype=dtype)
+
+    def decode_stacked(self, slots, out: Optional[torch.Tensor] = None, dtype: torch.dtype = torch.bfloat16
+                       ) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
+        """Decode-on-swap for decoded-mode serving: the selected slots decoded in one launch to
+        {module: (A (n, r, d_in), B (n, d_out, r))} views of one buffer (selection i = slots[i]),
+        the stacked factors ``PerSampleLoRALinear`` and ``per_sample_lora_delta`` take."""
+        sl = torch.as_tensor(slots, dtype=torch.int32).reshape(-1).to(self.device)
+        if self.num_slots == 0:
+            raise ValueError("bank is empty")
+        buf = decode_packed_stacked(self.words, sl, self.layout, self.pool_a, self.pool_b, out=out, dtype=dtype)
+        return split_stacked(buf, self.layout, sl.numel())
 
     def decode_diffusers(self, slot: int) -> Dict[str, Tuple[torch.Tensor, torch.Tensor, float]]:
         s = self.layout.scaling

@@ -161,6 +161,13 @@ class PackedLayout:
             self._sides_dev[key] = torch.from_numpy(table)
         return self._sides_dev[key]
 
+    def table_on(self, device) -> torch.Tensor:
+        """Device copy of ``ingest_table`` (read by the ingest and stacked-decode kernels)."""
+        key = "table:" + str(device)
+        if key not in self._sides_dev:
+            self._sides_dev[key] = self.ingest_table().to(device)
+        return self._sides_dev[key]
+
     def matches_modules(self, modules: Sequence[Dict], num_levels: int, block_size: int) -> bool:
         """True when ``modules`` ([{"name", "shape_a", "shape_b"}]) are this layout's, in order."""
         return (num_levels == self.num_levels and block_size == self.block_size and len(modules) == len(self.names)
@@ -283,6 +290,55 @@ def decode_int16(idx: torch.Tensor, layout: PackedLayout, pool_a: torch.Tensor,
     src.block_off = 0
     src.n_slots = 1
     return _decode(src, layout.total_blocks, layout.sides_on(idx.device), pool_a, pool_b, out)
+
+
+def decode_packed_stacked(bank: torch.Tensor, slots: torch.Tensor, layout: PackedLayout, pool_a: torch.Tensor,
+                          pool_b: torch.Tensor, out: Optional[torch.Tensor] = None,
+                          dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Decode the selected slots of a (n_slots, n_words) bank in one launch into the stacked
+    serving layout: a flat (n_sel * total_blocks * 64,) buffer in which every factor holds its
+    selections side by side (``split_stacked`` gives the per-module (n_sel, r, d_in) and
+    (n_sel, d_out, r) views that ``PerSampleLoRALinear`` would otherwise build with torch.stack)."""
+    _check_pools(pool_a, pool_b, layout)
+    _hip.require_gpu(bank, slots)
+    if bank.dim() != 2 or bank.shape[1] < layout.num_words:
+        raise ValueError("bank must be (n_slots, n_words >= layout.num_words)")
+    sl = slots.reshape(-1).to(torch.int32).contiguous()
+    n_sel = sl.numel()
+    numel = n_sel * layout.total_blocks * layout.block_size
+    if out is None:
+        out = torch.empty(numel, dtype=dtype, device=bank.device)
+    if out.numel() != numel or not out.is_contiguous() or out.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"out must be a contiguous bf16 / fp32 tensor of {numel} elements")
+    if n_sel == 0 or layout.total_blocks == 0:
+        return out
+    from ._delta import packed_source
+    src = packed_source(bank, layout.num_levels, 0)
+    table = layout.table_on(bank.device)
+    lut_a = _hip.lut_from_pools(pool_a, torch.float32)
+    lut_b = _hip.lut_from_pools(pool_b, torch.float32)
+    rc = _hip.load().lithe_decode_stacked(ctypes.byref(src), _hip.ptr(sl), n_sel, layout.total_blocks, table.shape[0],
+                                          _hip.ptr(table), _hip.ptr(layout.sides_on(bank.device)),
+                                          ctypes.byref(lut_a), ctypes.byref(lut_b), _hip.ptr(out),
+                                          _hip.dtype_code(out.dtype), None, _hip.stream_of(out.device))
+    _hip.check(rc, "lithe_decode_stacked")
+    return out
+
+
+def split_stacked(out: torch.Tensor, layout: PackedLayout, n_sel: int) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
+    """name -> (A (n_sel, r, d_in), B (n_sel, d_out, r)) views of a ``decode_packed_stacked`` buffer."""
+    flat = out.reshape(-1)
+    bs = layout.block_size
+    res = {}
+    for name, sa, sb, ao, bo in zip(layout.names, layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
+        na, nb = sa[0] * sa[1], sb[0] * sb[1]
+        nba, nbb = quant.num_blocks(sa, bs), quant.num_blocks(sb, bs)
+        if na != nba * bs or nb != nbb * bs:
+            raise ValueError(f"{name}: factors that do not fill whole blocks have no stacked view")
+        a = flat[n_sel * ao * bs: n_sel * (ao + nba) * bs].view(n_sel, sa[0], sa[1])
+        b = flat[n_sel * bo * bs: n_sel * (bo + nbb) * bs].view(n_sel, sb[0], sb[1])
+        res[name] = (a, b)
+    return res
 
 
 def split_decoded(out: torch.Tensor, layout: PackedLayout) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:

@@ -75,3 +75,21 @@ def prepare_packed(x: torch.Tensor, y: torch.Tensor, bank_words: torch.Tensor, a
     sl = slots.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
     return PreparedDelta(x, y, rank=rank, factors=f, route=_delta.routes(sl), accumulate=accumulate,
                          workspace=workspace, out_scale=scaling, keep=(sl, bank_words))
+
+
+def prepare_dense(x: torch.Tensor, y: torch.Tensor, a: torch.Tensor, b: torch.Tensor, slots: torch.Tensor, rank: int,
+                  scaling: float, workspace: torch.Tensor, accumulate: bool = True) -> PreparedDelta:
+    """Prepared decoded-mode delta: stacked dense factors ``a`` (n, r, d_in) and ``b``
+    (n, d_out, r) in the activation dtype (e.g. views from ``PackedBank.decode_stacked``);
+    sample i uses factor pair ``slots[i]``. Same kernels and rounding chain as the
+    index-resident call, so equal factors give bit-equal outputs."""
+    _hip.require_gpu(a, b)
+    if a.dtype != x.dtype or b.dtype != x.dtype or not a.is_contiguous() or not b.is_contiguous():
+        raise ValueError("dense factors must be contiguous and in the activation dtype")
+    if a.shape[0] != b.shape[0] or a.shape[1] != rank or b.shape[2] != rank or a.shape[2] != x.shape[2] \
+            or b.shape[1] != y.shape[2]:
+        raise ValueError(f"factor shapes {tuple(a.shape)}, {tuple(b.shape)} do not match x / y and rank {rank}")
+    f = _delta.dense_factors(a, b)
+    sl = slots.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
+    return PreparedDelta(x, y, rank=rank, factors=f, route=_delta.routes(sl), accumulate=accumulate,
+                         workspace=workspace, out_scale=scaling, keep=(sl, a, b))

@@ -1,0 +1,152 @@
+"""Decoded-mode serving on the GPU: one-launch decode-on-swap into stacked per-module factors
+(lithe_decode_stacked), bit-exact against per-slot decode + stack; the decoded-mode delta over
+those factors equals the index-resident delta bit for bit (same factors after the bf16 cast,
+same kernels and rounding chain)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from lithe_amd.kernels import PackedBank, _delta, _hip, split_decoded
+from lithe_amd.kernels.prepared import prepare_dense, prepare_packed, shared_workspace, workspace_bytes
+
+from helpers import SMALL, flux_modules, random_adapter
+
+pytestmark = pytest.mark.gpu
+
+
+def _bank(mods, n, seed):
+    ads = [random_adapter(mods, rank=16, seed=seed + s) for s in range(n)]
+    bank, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bank.add(w)
+    return ads, bank
+
+
+@pytest.mark.parametrize("mods,sel", [(SMALL, [2, 0, 2, 1]), (flux_modules(), [3, 1])])
+def test_decode_stacked_matches_per_slot_decode(mods, sel):
+    _, bank = _bank(mods, 4, 50)
+    st = bank.decode_stacked(sel)
+    torch.cuda.synchronize()
+    per = [bank.decode(s) for s in sel]
+    for name in bank.layout.names:
+        a, b = st[name]
+        assert a.is_contiguous() and b.is_contiguous()
+        assert torch.equal(a, torch.stack([p[name][0] for p in per]))
+        assert torch.equal(b, torch.stack([p[name][1] for p in per]))
+
+
+def test_decode_stacked_flags_an_inconsistent_table():
+    _, bank = _bank(SMALL, 2, 60)
+    lay = bank.layout
+    table = lay.ingest_table().clone()
+    table[-1, 1] += 1000                      # last factor claims more blocks than the layout has
+    tdev = table.cuda()
+    n_sel = 2
+    guard = 4096
+    out = torch.full((n_sel * lay.total_blocks * 64 + guard,), 7.0, dtype=torch.bfloat16, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    src = _delta.packed_source(bank.words, 3, 0)
+    lut_a = _hip.lut_from_pools(bank.pool_a, torch.float32)
+    lut_b = _hip.lut_from_pools(bank.pool_b, torch.float32)
+    slots = torch.tensor([0, 1], dtype=torch.int32, device="cuda")
+    rc = _hip.load().lithe_decode_stacked(ctypes.byref(src), _hip.ptr(slots), n_sel, lay.total_blocks,
+                                          table.shape[0], _hip.ptr(tdev), _hip.ptr(lay.sides_on("cuda")),
+                                          ctypes.byref(lut_a), ctypes.byref(lut_b), _hip.ptr(out),
+                                          _hip.DT_BF16, _hip.ptr(err), _hip.stream_of(out.device))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) & 4
+    assert (out[-guard:] == 7.0).all()        # nothing written past the output
+
+
+def test_decoded_mode_delta_matches_index_resident_and_oracle():
+    """(a) Factors decoded from pools rounded to bf16 are the index path's in-kernel factors
+    (shared.py casts the pools to the activation dtype before the level sum), so where both
+    plans give every wave a whole K range (d_in = 3072 with >= 2048 token groups) the dense
+    delta over them equals the index-resident delta bit for bit. Where K is split over waves
+    the dense plan cuts it at other points (4-block LDS pieces instead of 16 / 48), so only the
+    fp32 grouping differs. (b) Decoded mode proper (bulk decode with fp32 pools,
+    packed.py:205-222) on every shape against the oracle's LitheLinear chain (module.py:145-156:
+    x A^T, then B^T, then * scaling, then + base, each rounded to bf16)."""
+    from lithe_amd.kernels import decode_packed_stacked, split_stacked
+    from oracle import codebook as ocb
+    from oracle import decode as odec
+    from oracle import delta as odelta
+    from helpers import rel, to_np
+    mods = [("q", 3072, 3072), ("up", 3072, 12288), ("down", 12288, 3072)]
+    ads, bank = _bank(mods, 5, 70)
+    slot_list = [4, 1, 1, 0]
+    slots = torch.tensor(slot_list, dtype=torch.int32, device="cuda")
+    uniq = [4, 1, 0]
+    sel = torch.tensor([uniq.index(s) for s in slot_list], dtype=torch.int32, device="cuda")
+    u = torch.tensor(uniq, dtype=torch.int32, device="cuda")
+    rp = (bank.pool_a.bfloat16().float(), bank.pool_b.bfloat16().float())
+    st_bf = split_stacked(decode_packed_stacked(bank.words, u, bank.layout, *rp), bank.layout, len(uniq))
+    st = bank.decode_stacked(uniq)
+    pools = (bank.pool_a.bfloat16(), bank.pool_b.bfloat16())
+    gen = torch.Generator(device="cuda").manual_seed(3)
+
+    def run(name, di, do, seq):
+        x = torch.randn(4, seq, di, device="cuda", generator=gen).bfloat16()
+        y0 = torch.randn(4, seq, do, device="cuda", generator=gen).bfloat16()
+        ws = shared_workspace("cuda", workspace_bytes((4, seq, di), do, 16, 1, torch.bfloat16))
+        _, _, _, a_off, b_off = bank.layout.module(name)
+        yi, yb, yd = y0.clone(), y0.clone(), y0.clone()
+        prepare_packed(x, yi, bank.words, a_off, b_off, 3, pools, slots, 16, 0.75, ws)()
+        prepare_dense(x, yb, st_bf[name][0], st_bf[name][1], sel, 16, 0.75, ws)()
+        prepare_dense(x, yd, st[name][0], st[name][1], sel, 16, 0.75, ws)()
+        torch.cuda.synchronize()
+        return x, y0, yi, yb, yd
+
+    for name, di, do in mods[:2]:
+        _, y0, yi, yb, _ = run(name, di, do, 8192)
+        assert torch.equal(yi, yb), name
+        assert not torch.equal(yi, y0)
+    pa, pb = ocb.twin_pools()
+    for name, di, do in mods:
+        for seq in (77, 130):
+            x, y0, yi, yb, yd = run(name, di, do, seq)
+            assert rel(to_np(yb), to_np(yi)) < 2e-3, (name, seq)
+            got, xn, y0n = to_np(yd), to_np(x), to_np(y0)
+            for i, s in enumerate(slot_list):
+                a = odec.decode(ads[s].indices[name]["A"], (16, di), pa)
+                b = odec.decode(ads[s].indices[name]["B"], (do, 16), pb)
+                want = odelta.lithe_linear(xn[i], y0n[i], a, b, 0.75, "bf16")
+                assert rel(got[i], want) < 2e-3, (name, seq, i)
+                assert rel(got[i] - y0n[i], want - y0n[i]) < 5e-2, (name, seq, i)   # the delta itself
+
+
+def test_decode_stacked_from_int16_source_matches_packed():
+    """The generic kernel (unpacked index kinds) writes the same stacked layout: block-major int16
+    indices of three adapters (decode_int16's source) against the packed bank's stacked decode."""
+    from lithe_amd.kernels import flat_indices
+    ads, bank = _bank(SMALL, 3, 80)
+    lay = bank.layout
+    sel = [1, 2, 0, 1]
+    want = bank.decode_stacked(sel)
+    idx = torch.from_numpy(np.stack([flat_indices(ad, lay).astype(np.int16) for ad in ads])).cuda()
+    src = _hip.IndexSrc()
+    src.base = idx.data_ptr()
+    src.kind = _hip.IDX_BLOCK_I16
+    src.num_levels = 3
+    src.slot_stride = idx.stride(0)
+    src.level_stride = 0
+    src.block_off = 0
+    src.n_slots = 3
+    out = torch.empty(len(sel) * lay.total_blocks * 64, dtype=torch.bfloat16, device="cuda")
+    slots = torch.tensor(sel, dtype=torch.int32, device="cuda")
+    lut_a = _hip.lut_from_pools(bank.pool_a, torch.float32)
+    lut_b = _hip.lut_from_pools(bank.pool_b, torch.float32)
+    table = lay.table_on("cuda")
+    rc = _hip.load().lithe_decode_stacked(ctypes.byref(src), _hip.ptr(slots), len(sel), lay.total_blocks,
+                                          table.shape[0], _hip.ptr(table), _hip.ptr(lay.sides_on("cuda")),
+                                          ctypes.byref(lut_a), ctypes.byref(lut_b), _hip.ptr(out), _hip.DT_BF16,
+                                          None, _hip.stream_of(out.device))
+    assert rc == 0
+    from lithe_amd.kernels import split_stacked
+    got = split_stacked(out, lay, len(sel))
+    torch.cuda.synchronize()
+    for name in lay.names:
+        assert torch.equal(got[name][0], want[name][0]) and torch.equal(got[name][1], want[name][1])
