@@ -936,7 +936,9 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // are as long as the fill batch allows; a factor that fits one piece gets one region.
     const int pad = 16 / xbytes;
     if (dense) {
-        p.pb = std::max(1, 4 / p.GM);
+        // dense rows are 4x the LDS of periods: 4-block pieces with whole-K waves, 12 when K is
+        // split over 4 waves (measured over the FLUX shapes)
+        p.pb = std::max(1, (ks >= 4 ? 12 : 4) / p.GM);
         p.arow = p.pb * kBlock + pad;
     } else {
         // Few token groups (K split over 4 waves): one long piece (fewer barriers) wins; with
@@ -945,9 +947,9 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
         p.pb = std::max(1, std::min(ks >= 4 ? 48 : 16, kFillBatch * kThreads / (p.GM * 16)));
         p.arow = p.pb * 16 + pad;
     }
-    if (getenv("LITHE_SHRINK_PB") && !dense) {
+    if (getenv("LITHE_SHRINK_PB")) {
         p.pb = std::max(1, std::min(env_int("LITHE_SHRINK_PB", p.pb), kFillBatch * kThreads / (p.GM * 16)));
-        p.arow = p.pb * 16 + pad;
+        p.arow = p.pb * (dense ? kBlock : 16) + pad;
     }
     p.region = p.GM * 16 * p.arow;
     const int64_t npiece = (d_in / kBlock + p.pb - 1) / p.pb;
