@@ -57,12 +57,13 @@ def flux_modules(img_tokens: int, txt_tokens: int):
 class Workload:
     """Bank, buffers and prepared per-module calls of one configuration."""
 
-    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0, decoded=False):
+    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0, decoded=False, qkv=False):
         import numpy as np
         import torch
 
         from lithe_amd.kernels import PackedBank, PackedLayout
-        from lithe_amd.kernels.prepared import prepare_dense, prepare_packed, shared_workspace, workspace_bytes
+        from lithe_amd.kernels.prepared import (prepare_dense, prepare_packed, prepare_packed_shared_x,
+                                                shared_workspace, workspace_bytes)
 
         self.name, self.mods, self.batch = name, mods, batch
         dev = torch.device("cuda:0")
@@ -92,9 +93,10 @@ class Workload:
             self._next[key] = (i + 1) % len(self._bufs[key])
             return self._bufs[key][i]
 
-        need = max(workspace_bytes((batch, m, di), do, RANK, 1, torch.bfloat16) for _, di, do, m in mods)
+        need = max(workspace_bytes((batch, m, di), do, RANK, 3 if qkv else 1, torch.bfloat16) for _, di, do, m in mods)
         self.workspace = shared_workspace(dev, need)
         self.calls = []
+        self.call_mods = []
         uniq = sorted(set(np.asarray(assign).tolist()))
         self.decode_ms = None
         if decoded:
@@ -108,7 +110,22 @@ class Workload:
             self.factors = self.bank.decode_stacked(uniq)
             torch.cuda.synchronize()
             self.decode_ms = (time.perf_counter() - t0) * 1e3
-        for n, di, do, m in mods:
+        k = 0
+        while k < len(mods):
+            n, di, do, m = mods[k]
+            if qkv and (n.endswith("attn.to_q") or n.endswith("attn.add_q_proj")):
+                # the three projections of one attention input read the same x
+                group = mods[k:k + 3]
+                x = buf(di, m)
+                ys = [buf(g[2], g[3]) for g in group]
+                offs = [layout.module(g[0])[3:5] for g in group]
+                self.calls.append(prepare_packed_shared_x(x, ys, self.bank.words, offs, 3, pools, self.assign, RANK,
+                                                          1.0, self.workspace, accumulate=True))
+                self.call_mods.append(group)
+                k += 3
+                continue
+            k += 1
+            self.call_mods.append([mods[k - 1]])
             _, _, _, a_off, b_off = layout.module(n)
             x, y = buf(di, m), buf(do, m)
             if decoded:
@@ -471,7 +488,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="flux342", choices=["flux342", "decoded", "ffn", "hb", "decode", "ingest"])
+    ap.add_argument("--config", default="flux342",
+                    choices=["flux342", "qkv", "decoded", "ffn", "hb", "decode", "ingest"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -497,14 +515,18 @@ def main():
         run_ingest(args)
         return
     rng = np.random.default_rng(1234)
-    if args.config in ("flux342", "decoded"):
+    if args.config in ("flux342", "decoded", "qkv"):
         mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
         assign = rng.choice(n_slots, batch, replace=False)
-        wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config == "decoded")
+        wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config == "decoded",
+                      qkv=args.config == "qkv")
         workload = "FLUX.1-dev 342 linears, 1024^2: B=14 x 4608 tokens (4096 img + 512 txt), 10k-adapter packed bank"
         if args.config == "decoded":
             workload += (", decoded mode: the 14 routed adapters decoded once to stacked bf16 factors "
                          "(decode-on-swap), modules read dense factors")
+        if args.config == "qkv":
+            workload += (", q/k/v fused: the three projections of each attention input read x once "
+                         f"({len(wl.calls)} calls per sweep)")
     elif args.config == "hb":
         mods, batch, n_slots = flux_modules(256, 512), 96, args.slots or 10_000
         ranks = np.arange(1, n_slots + 1, dtype=np.float64)
@@ -530,8 +552,9 @@ def main():
     call_ms = sum(per)
     achieved = wl.alg_bytes / (call_ms * 1e-3) / 1e9
     classes = {}
-    for (n, di, do, m), t, c in zip(wl.mods, per, wl.calls):
-        k = f"{di}->{do} x {m}"
+    for group, t, c in zip(wl.call_mods, per, wl.calls):
+        _, di, do, m = group[0]
+        k = f"{di}->{do} x {m}" if len(group) == 1 else f"{di}->{len(group)}x{do} x {m} (shared x)"
         e = classes.setdefault(k, {"count": 0, "ms": 0.0, "bytes": 0})
         e["count"] += 1
         e["ms"] += t
@@ -562,10 +585,13 @@ def main():
         "data": "synthetic",
         "config": {"workload": workload, "modules": len(wl.mods), "global_batch": batch,
                    "tokens_per_step": tokens, "rank": RANK, "bank_slots": n_slots,
-                   "bank_GB": round(wl.bank.words.numel() * 8 / 1e9, 2), "hip_graph": graphed},
+                   "bank_GB": round(wl.bank.words.numel() * 8 / 1e9, 2), "hip_graph": graphed,
+                   "calls_per_step": len(wl.calls)},
         "achieved_GBps": round(wl.alg_bytes / (ms * 1e-3) / 1e9, 1),
         "frac_of_peak": round(wl.alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-        "roofline": {"kernel": "lithe_lora_delta (shrink + expand, one call per module)", "bound": "hbm",
+        "roofline": {"kernel": "lithe_lora_delta (shrink + expand, one call per module)" if args.config != "qkv"
+                     else "lithe_lora_delta / lithe_lora_delta_shared_x (one shrink + one expand per module)",
+                     "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_step": wl.alg_bytes,

@@ -201,6 +201,26 @@ int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_
                          const float *mid_scale, float out_scale, const float *out_scale_vec,
                          void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Shared-input group: n_mod modules whose linears read the same x (the to_q / to_k / to_v
+ * projections of a FLUX attention block, or add_q / add_k / add_v_proj). One shrink reads x once
+ * and produces the rank-r intermediate of every module (mid = x [A_0; A_1; ...]^T, stacked as
+ * rank groups), then one expand per module updates y[m] (n_batch, seq, d_out[m]) exactly as
+ * lithe_lora_delta would with out_scale[m] (no out_scale_vec). Factors: n_mod INDEXED entries
+ * that share one A index source (base, kind, levels, strides, n_slots; each module's A at its
+ * own block_off) and one A value table; each module has its own B source and B table.
+ * y, d_out, out_scale and factors are host arrays of n_mod entries (y[m] a device pointer).
+ * n_mod * ceil(rank / 16) * n_route <= 8. Workspace: lithe_lora_workspace_bytes(n_batch, seq,
+ * d_in, max d_out, rank, n_route * n_mod, x_dtype). LITHE_ERR_UNSUPPORTED if the A sources or
+ * A tables differ, or a factor is DENSE.
+ * Replaces three shared_codebook_lora_delta calls over one input (lithe/kernels/shared.py:197-263
+ * via IndexLoRALinear.forward, lithe/kernels/layers.py:120-131), the q/k/v fusion of
+ * wrap_index (serving/_common.py:294-311). */
+int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
+                                  int32_t n_mod, void *const *y, int32_t y_dtype, const int64_t *d_out,
+                                  int32_t accumulate, int32_t rank, const lithe_factors *factors,
+                                  const lithe_routes *routes, const float *mid_scale, const float *out_scale,
+                                  void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Reads the in-kernel error word of a workspace (slot id out of range, index > 511) into
  * *flags on the host; synchronises the stream. 0 = no error since the last clear. */
 int32_t lithe_workspace_errors(const void *workspace, int32_t *flags, int32_t clear, void *stream);

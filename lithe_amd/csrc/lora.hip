@@ -81,6 +81,16 @@ struct LoraArgs {
     const float *mid_scale;
     const float *out_scale_vec;
     IdxSrc a_src, b_src;
+    // Shared-input calls: the shrink's G groups are (module, route entry, rank group), module
+    // m = g / G1; group g's A blocks start at a_goff[g] (a_src.block_off is 0 in the kernels).
+    // The expand of one module reads mid groups [mid_goff, mid_goff + G).
+    int64_t a_goff[kMaxGroups];
+    int32_t G1, mid_goff;
+    // Replicated shared-input shrink: n_mod_wg > 1 launches one workgroup per (token tile, module),
+    // the modules of a tile on consecutive workgroup ids, so x is fetched from HBM once and the
+    // other modules' reads hit the Infinity Cache. Module mod's groups start at a_goff[mod]
+    // and write mid groups [mod * G, (mod + 1) * G).
+    int32_t n_mod_wg;
     Luts luts;
     const void *dense_a, *dense_b;
     int64_t n_slots;
@@ -172,7 +182,16 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
     const int ks = a.ks, tgw = kWaves / a.ks;
     const int tgi = wave % tgw, ksi = wave / tgw;
-    const int tile = blockIdx.x;
+    // Replicated mode: workgroups are dealt round-robin to the 8 XCDs, so id w runs on XCD w % 8.
+    // The modules of tile t sit at ids 8 (M (t / 8) + m) + t % 8: one XCD, consecutive in its
+    // queue, sharing that XCD's L2 for x.
+    int mod = 0, tile = (int)blockIdx.x;
+    if (a.n_mod_wg > 1) {
+        const int q = (int)(blockIdx.x >> 3);
+        mod = q % a.n_mod_wg;
+        tile = (q / a.n_mod_wg) * 8 + (int)(blockIdx.x & 7);
+        if (tile >= (int)a.n_batch * a.tiles_s) return;    // padding of the last XCD round (before any barrier)
+    }
     const int64_t b = tile / a.tiles_s;
     const int mt = tile % a.tiles_s;
     const int64_t m = ((int64_t)mt * tgw + tgi) * 16 + r16;
@@ -190,12 +209,12 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     bool any = false;
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-        const int j = (g < a.G ? g : 0) / a.n_rg;
+        const int j = ((g < a.G ? g : 0) % a.G1) / a.n_rg;
         gs[g] = g < a.G ? (int32_t)route_slot(a, b, j, false) : -1;
         gw[g] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
         any = any || gs[g] >= 0;
     }
-    if (tid < GM && tid < a.G) route_slot(a, b, tid / a.n_rg, true);   // records bad slot ids
+    if (tid < GM && tid < a.G) route_slot(a, b, (tid % a.G1) / a.n_rg, true);   // records bad slot ids
     if (!any) return;    // no adapter on this sample: no mid row is read for it
     auto group_slot = [&](int g) __attribute__((always_inline)) -> int32_t {    // gs[g] for a run-time g < GM
         int32_t r = gs[0];
@@ -213,6 +232,17 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
         int r = 0;
 #pragma unroll
         for (int q = 1; q < GM; ++q) r = g == q ? (q % a.n_rg) * 16 : r;
+        return r;
+    };
+    // module of this workgroup's A in replicated mode (uniform), a_goff[mod]
+    int64_t mod_aoff = a.a_goff[0];
+#pragma unroll
+    for (int q = 1; q < kMaxGroups; ++q) mod_aoff = mod == q ? a.a_goff[q] : mod_aoff;
+    auto group_aoff = [&](int g) __attribute__((always_inline)) -> int64_t {   // a_goff[g], branch-free
+        if (a.n_mod_wg > 1) return mod_aoff;
+        int64_t r = a.a_goff[0];
+#pragma unroll
+        for (int q = 1; q < GM; ++q) r = g == q ? a.a_goff[q] : r;
         return r;
     };
     if constexpr (SRC != SRC_DENSE) stage_lut(lut, a.luts.v[0][0], tid);
@@ -233,7 +263,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
         const int grp = gr >> 4;
         const int rr = group_rank0(grp) + (gr & 15);
         live = group_slot(grp) >= 0 && rr < a.rank;
-        return live ? (int64_t)rr * nb + (int64_t)g * pb + c : 0;
+        return live ? group_aoff(grp) + (int64_t)rr * nb + (int64_t)g * pb + c : 0;
     };
     auto idx_load = [&](int g, RawIdx *dst) __attribute__((always_inline)) {
         if (g >= npiece) return;
@@ -494,7 +524,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
         if (gs[g] < 0) continue;
-        XT *dst = static_cast<XT *>(a.mid) + row * a.MR + g * 16 + 4 * gq;
+        XT *dst = static_cast<XT *>(a.mid) + row * a.MR + (mod * a.G + g) * 16 + 4 * gq;
         if constexpr (kBf16) {
             bf16x4 o;
 #pragma unroll
@@ -832,7 +862,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
         Frag mf[GM];
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
-            const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + gsrc[g] * 16 + 4 * gq;
+            const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + (a.mid_goff + gsrc[g]) * 16 + 4 * gq;
             if constexpr (sizeof(XT) == 2) mf[g] = *reinterpret_cast<const i16x4 *>(src);
             else mf[g] = *reinterpret_cast<const f32x4 *>(src);
         }
@@ -922,7 +952,10 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // shrink: one wave per 16 tokens x (K / ks); ks grows until there are enough waves.
     const int64_t groups = n_batch * ((seq + 15) / 16);
     int ks = 1;
-    while (ks < 4 && (groups * ks < target || d_in / ks > 6144)) ks *= 2;   // long K: shorter per-wave streams
+    // long K: shorter per-wave streams; with 4 or 8 rank groups a 4-way split costs more in
+    // LDS reads than it gains (measured on the q/k/v shared-input shapes)
+    const int ks_max = p.GM >= 4 ? 2 : 4;
+    while (ks < ks_max && (groups * ks < target || d_in / ks > 6144)) ks *= 2;
     if (getenv("LITHE_SHRINK_KS")) {
         const int v = env_int("LITHE_SHRINK_KS", ks);
         ks = v >= 4 ? 4 : v >= 2 ? 2 : 1;
@@ -984,10 +1017,16 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     return p;
 }
 
-template <typename XT, typename YT, int SRC, int GM, int BOM, int U>
-void launch(const Plan &p, LoraArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, U>), dim3((unsigned)(a.n_batch * p.tiles_s)), dim3(kThreads),
-                       p.lds_s, st, a);
+template <typename XT, int SRC, int GM>
+void launch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU>),
+                       dim3((unsigned)(a.n_mod_wg > 1 ? (a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg
+                                                      : a.n_batch * p.tiles_s)),
+                       dim3(kThreads), p.lds_s, st, a);
+}
+
+template <typename XT, typename YT, int SRC, int GM, int BOM>
+void launch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
     dim3 ge((unsigned)(((a.d_out + p.BO - 1) / p.BO) * a.n_batch * p.tiles_e));
     const bool quad = (a.rank & 3) == 0;
     if constexpr (GM == 1 && sizeof(YT) == 2) {
@@ -1008,24 +1047,79 @@ void launch(const Plan &p, LoraArgs &a, hipStream_t st) {
     }
 }
 
+template <typename XT, int SRC>
+void dispatch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
+    switch (p.GM) {
+        case 1: launch_shrink<XT, SRC, 1>(p, a, st); break;
+        case 2: launch_shrink<XT, SRC, 2>(p, a, st); break;
+        case 4: launch_shrink<XT, SRC, 4>(p, a, st); break;
+        default: launch_shrink<XT, SRC, 8>(p, a, st); break;
+    }
+}
+
+// expand output tiles: BOM outputs per workgroup (make_plan's bo_max for the same GM)
 template <typename XT, typename YT, int SRC>
-int32_t dispatch_gm(const Plan &p, LoraArgs &a, hipStream_t st) {
+void dispatch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
     constexpr bool bf = sizeof(XT) == 2;
     switch (p.GM) {
-        case 1: launch<XT, YT, SRC, 1, bf ? 256 : 128, kShrinkU>(p, a, st); break;
-        case 2: launch<XT, YT, SRC, 2, bf ? 256 : 128, kShrinkU>(p, a, st); break;
-        case 4: launch<XT, YT, SRC, 4, bf ? 128 : 64, kShrinkU>(p, a, st); break;
-        default: launch<XT, YT, SRC, 8, bf ? 64 : 32, kShrinkU>(p, a, st); break;
+        case 1: launch_expand<XT, YT, SRC, 1, bf ? 256 : 128>(p, a, st); break;
+        case 2: launch_expand<XT, YT, SRC, 2, bf ? 256 : 128>(p, a, st); break;
+        case 4: launch_expand<XT, YT, SRC, 4, bf ? 128 : 64>(p, a, st); break;
+        default: launch_expand<XT, YT, SRC, 8, bf ? 64 : 32>(p, a, st); break;
     }
-    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+int src_of(const LoraArgs &a, int kind) {
+    if (kind == LITHE_FACTOR_DENSE) return SRC_DENSE;
+    if (a.a_src.kind == LITHE_IDX_PACKED9 && a.b_src.kind == LITHE_IDX_PACKED9 && a.a_src.levels == kPackedLevels)
+        return SRC_PACKED;
+    return SRC_INDEXED;
 }
 
 template <typename XT, typename YT>
-int32_t dispatch_src(const Plan &p, LoraArgs &a, int kind, hipStream_t st) {
-    if (kind == LITHE_FACTOR_DENSE) return dispatch_gm<XT, YT, SRC_DENSE>(p, a, st);
-    if (a.a_src.kind == LITHE_IDX_PACKED9 && a.b_src.kind == LITHE_IDX_PACKED9 && a.a_src.levels == kPackedLevels)
-        return dispatch_gm<XT, YT, SRC_PACKED>(p, a, st);
-    return dispatch_gm<XT, YT, SRC_INDEXED>(p, a, st);
+void dispatch(bool shrink, const Plan &p, const LoraArgs &a, int src, hipStream_t st) {
+    if (shrink) {
+        if (src == SRC_DENSE) dispatch_shrink<XT, SRC_DENSE>(p, a, st);
+        else if (src == SRC_PACKED) dispatch_shrink<XT, SRC_PACKED>(p, a, st);
+        else dispatch_shrink<XT, SRC_INDEXED>(p, a, st);
+    } else {
+        if (src == SRC_DENSE) dispatch_expand<XT, YT, SRC_DENSE>(p, a, st);
+        else if (src == SRC_PACKED) dispatch_expand<XT, YT, SRC_PACKED>(p, a, st);
+        else dispatch_expand<XT, YT, SRC_INDEXED>(p, a, st);
+    }
+}
+
+void launch_typed(bool shrink, int x_dtype, int y_dtype, const Plan &p, const LoraArgs &a, int src, hipStream_t st) {
+    if (x_dtype == LITHE_DT_BF16) {
+        if (y_dtype == LITHE_DT_BF16) dispatch<__bf16, __bf16>(shrink, p, a, src, st);
+        else dispatch<__bf16, float>(shrink, p, a, src, st);
+    } else {
+        if (y_dtype == LITHE_DT_BF16) dispatch<float, __bf16>(shrink, p, a, src, st);
+        else dispatch<float, float>(shrink, p, a, src, st);
+    }
+}
+
+// Copies a plan's shrink fields into the kernel arguments.
+void set_shrink_fields(LoraArgs &a, const Plan &p) {
+    a.G = p.G;
+    a.n_rg = p.n_rg;
+    a.MR = p.MR;
+    a.tiles_s = p.tiles_s;
+    a.ks = p.ks;
+    a.pb = p.pb;
+    a.arow = p.arow;
+    a.region = p.region;
+    a.red_off = p.red_off;
+    a.stage_off = p.stage_off;
+}
+
+// Copies a plan's expand fields into the kernel arguments.
+void set_expand_fields(LoraArgs &a, const Plan &p) {
+    a.tiles_e = p.tiles_e;
+    a.subs_e = p.subs_e;
+    a.BO = p.BO;
+    a.nblk_max = p.nblk_max;
+    a.estage_off = p.estage_off;
 }
 
 }  // namespace
@@ -1042,46 +1136,104 @@ extern "C" int64_t lithe_lora_workspace_bytes(int64_t n_batch, int64_t seq, int6
     return make_plan(n_batch, seq, d_in, d_out, rank, n_route, x_dtype == LITHE_DT_BF16 ? 2 : 4, false).total;
 }
 
+namespace lithe {
+namespace {
+
+// Checks shared by both delta entry points (sizes, dtypes, alignment of x and the workspace).
+int32_t check_call(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in, int32_t y_dtype,
+                   int32_t rank, const lithe_routes *routes, int groups_per_module, int n_mod, const void *workspace) {
+    if (!routes) return LITHE_ERR_NULL;
+    if (x_dtype != LITHE_DT_BF16 && x_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
+    if (y_dtype != LITHE_DT_BF16 && y_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
+    if (n_batch < 0 || seq < 0 || d_in < 1 || rank < 1 || routes->n_route < 1) return LITHE_ERR_SHAPE;
+    if (n_batch > 65535 || seq > (int64_t)1 << 30) return LITHE_ERR_SHAPE;
+    if (d_in % kBlock) return LITHE_ERR_ALIGN;
+    if ((int64_t)groups_per_module * routes->n_route * n_mod > kMaxGroups) return LITHE_ERR_SHAPE;
+    if (n_batch == 0 || seq == 0) return LITHE_OK;
+    if (!x || !routes->slot) return LITHE_ERR_NULL;
+    if (!workspace) return LITHE_ERR_WORKSPACE;
+    if (((uintptr_t)x & 15u) || ((uintptr_t)workspace & 255u)) return LITHE_ERR_ALIGN;
+    return LITHE_OK;
+}
+
+// Validates indexed factors of one module (A over rank x d_in, B over d_out x rank).
+int32_t check_indexed(const lithe_factors *f, int32_t rank, int64_t d_in, int64_t d_out) {
+    int32_t rc = validate_src(&f->a_idx);
+    if (rc) return rc;
+    rc = validate_src(&f->b_idx);
+    if (rc) return rc;
+    if (f->a_idx.num_levels != f->b_idx.num_levels || f->lut_a.num_levels != f->a_idx.num_levels ||
+        f->lut_b.num_levels != f->a_idx.num_levels)
+        return LITHE_ERR_LEVELS;
+    if (!src_covers(f->a_idx, rank * d_in / kBlock) || !src_covers(f->b_idx, d_out * rank / kBlock))
+        return LITHE_ERR_SHAPE;
+    return LITHE_OK;
+}
+
+void copy_lut(float dst[kMaxLevels][10], const lithe_lut &l) {
+    for (int v = 0; v < kMaxLevels; ++v)
+        for (int q = 0; q < 10; ++q) dst[v][q] = l.value[v][q];
+}
+
+// Fields common to the shrink and the expand of a call.
+void set_call_fields(LoraArgs &a, const void *x, char *ws, const Plan &p, int64_t n_batch, int64_t seq, int64_t d_in,
+                     int32_t rank, const lithe_routes *routes, const float *mid_scale) {
+    a.x = x;
+    a.err = reinterpret_cast<int32_t *>(ws);
+    a.mid = ws + p.off_mid;
+    a.n_batch = n_batch;
+    a.seq = seq;
+    a.d_in = d_in;
+    a.rows = n_batch * seq;
+    a.rank = rank;
+    a.n_route = routes->n_route;
+    a.r_slot = routes->slot;
+    a.r_w = routes->weight_sqrt;
+    a.s_scale = routes->slot_scale;
+    a.mid_scale = mid_scale;
+}
+
+// Fields of one module's expand.
+void set_module_fields(LoraArgs &a, void *y, int64_t d_out, int32_t accumulate, float out_scale,
+                       const float *out_scale_vec) {
+    a.y = y;
+    a.d_out = d_out;
+    a.vec_y = (d_out % 8 == 0) && (((uintptr_t)y & 15u) == 0);
+    a.accumulate = accumulate ? 1 : 0;
+    a.out_scale = out_scale;
+    a.out_scale_vec = out_scale_vec;
+}
+
+}  // namespace
+}  // namespace lithe
+
 extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
                                     void *y, int32_t y_dtype, int64_t d_out, int32_t accumulate, int32_t rank,
                                     const lithe_factors *f, const lithe_routes *routes, const float *mid_scale,
                                     float out_scale, const float *out_scale_vec, void *workspace,
                                     int64_t workspace_bytes, void *stream) {
-    if (!f || !routes) return LITHE_ERR_NULL;
-    if (x_dtype != LITHE_DT_BF16 && x_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
-    if (y_dtype != LITHE_DT_BF16 && y_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
-    if (n_batch < 0 || seq < 0 || d_in < 1 || d_out < 1 || rank < 1 || routes->n_route < 1) return LITHE_ERR_SHAPE;
-    if (n_batch > 65535 || seq > (int64_t)1 << 30) return LITHE_ERR_SHAPE;
-    if (d_in % kBlock || (d_out * rank) % kBlock) return LITHE_ERR_ALIGN;
-    const int n_rg = (rank + 15) / 16;
-    if (n_rg * routes->n_route > kMaxGroups) return LITHE_ERR_SHAPE;
-    if (n_batch == 0 || seq == 0) return LITHE_OK;
-    if (!x || !y || !routes->slot) return LITHE_ERR_NULL;
-    if (!workspace) return LITHE_ERR_WORKSPACE;
+    if (!f) return LITHE_ERR_NULL;
+    const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
+    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, 1, workspace);
+    if (rc || n_batch == 0 || seq == 0) return rc;
+    if (d_out < 1) return LITHE_ERR_SHAPE;
+    if ((d_out * rank) % kBlock) return LITHE_ERR_ALIGN;
+    if (!y) return LITHE_ERR_NULL;
     const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
     const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
-    if (((uintptr_t)x & 15u) || ((uintptr_t)workspace & 255u)) return LITHE_ERR_ALIGN;
     if ((uintptr_t)y & (uintptr_t)(ybytes - 1)) return LITHE_ERR_ALIGN;
 
     LoraArgs a{};
     if (f->kind == LITHE_FACTOR_INDEXED) {
-        int32_t rc = validate_src(&f->a_idx);
+        rc = check_indexed(f, rank, d_in, d_out);
         if (rc) return rc;
-        rc = validate_src(&f->b_idx);
-        if (rc) return rc;
-        if (f->a_idx.num_levels != f->b_idx.num_levels || f->lut_a.num_levels != f->a_idx.num_levels ||
-            f->lut_b.num_levels != f->a_idx.num_levels)
-            return LITHE_ERR_LEVELS;
-        if (!src_covers(f->a_idx, rank * d_in / kBlock) || !src_covers(f->b_idx, d_out * rank / kBlock))
-            return LITHE_ERR_SHAPE;
         a.a_src = make_src(f->a_idx);
         a.b_src = make_src(f->b_idx);
+        for (int g = 0; g < kMaxGroups; ++g) a.a_goff[g] = a.a_src.block_off;
+        a.a_src.block_off = 0;
         a.n_slots = std::min(f->a_idx.n_slots, f->b_idx.n_slots);
-        for (int l = 0; l < kMaxLevels; ++l)
-            for (int q = 0; q < 10; ++q) {
-                a.luts.v[0][l][q] = f->lut_a.value[l][q];
-                a.luts.v[1][l][q] = f->lut_b.value[l][q];
-            }
+        copy_lut(a.luts.v[0], f->lut_a);
+        copy_lut(a.luts.v[1], f->lut_b);
     } else if (f->kind == LITHE_FACTOR_DENSE) {
         if (!f->dense_a || !f->dense_b) return LITHE_ERR_NULL;
         if (f->dense_dtype != x_dtype) return LITHE_ERR_DTYPE;
@@ -1098,50 +1250,95 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     const Plan p = make_plan(n_batch, seq, d_in, d_out, rank, routes->n_route, xbytes, f->kind == LITHE_FACTOR_DENSE,
                              ybytes);
     if (workspace_bytes < p.total) return LITHE_ERR_WORKSPACE;
-
-    char *ws = static_cast<char *>(workspace);
-    a.x = x;
-    a.y = y;
-    a.err = reinterpret_cast<int32_t *>(ws);
-    a.mid = ws + p.off_mid;
-    a.n_batch = n_batch;
-    a.seq = seq;
-    a.d_in = d_in;
-    a.d_out = d_out;
-    a.rows = n_batch * seq;
-    a.rank = rank;
-    a.G = p.G;
-    a.n_rg = p.n_rg;
-    a.n_route = routes->n_route;
-    a.MR = p.MR;
-    a.tiles_s = p.tiles_s;
-    a.ks = p.ks;
-    a.pb = p.pb;
-    a.arow = p.arow;
-    a.region = p.region;
-    a.red_off = p.red_off;
-    a.stage_off = p.stage_off;
-    a.tiles_e = p.tiles_e;
-    a.subs_e = p.subs_e;
-    a.BO = p.BO;
-    a.nblk_max = p.nblk_max;
-    a.estage_off = p.estage_off;
-    a.vec_y = (d_out % 8 == 0) && (((uintptr_t)y & 15u) == 0);
-    a.accumulate = accumulate ? 1 : 0;
-    a.out_scale = out_scale;
-    a.r_slot = routes->slot;
-    a.r_w = routes->weight_sqrt;
-    a.s_scale = routes->slot_scale;
-    a.mid_scale = mid_scale;
-    a.out_scale_vec = out_scale_vec;
-
+    set_call_fields(a, x, static_cast<char *>(workspace), p, n_batch, seq, d_in, rank, routes, mid_scale);
+    set_module_fields(a, y, d_out, accumulate, out_scale, out_scale_vec);
+    set_shrink_fields(a, p);
+    set_expand_fields(a, p);
+    a.G1 = p.G;
+    a.mid_goff = 0;
+    const int src = src_of(a, f->kind);
     hipStream_t st = (hipStream_t)stream;
-    if (x_dtype == LITHE_DT_BF16) {
-        return y_dtype == LITHE_DT_BF16 ? dispatch_src<__bf16, __bf16>(p, a, f->kind, st)
-                                        : dispatch_src<__bf16, float>(p, a, f->kind, st);
+    launch_typed(true, x_dtype, y_dtype, p, a, src, st);
+    launch_typed(false, x_dtype, y_dtype, p, a, src, st);
+    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq,
+                                             int64_t d_in, int32_t n_mod, void *const *y, int32_t y_dtype,
+                                             const int64_t *d_out, int32_t accumulate, int32_t rank,
+                                             const lithe_factors *f, const lithe_routes *routes,
+                                             const float *mid_scale, const float *out_scale, void *workspace,
+                                             int64_t workspace_bytes, void *stream) {
+    if (!f || !y || !d_out || !out_scale) return LITHE_ERR_NULL;
+    if (n_mod < 1) return LITHE_ERR_SHAPE;
+    const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
+    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, n_mod, workspace);
+    if (rc || n_batch == 0 || seq == 0) return rc;
+    const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
+    const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
+    int64_t d_out_max = 1;
+    for (int m = 0; m < n_mod; ++m) {
+        if (f[m].kind != LITHE_FACTOR_INDEXED) return LITHE_ERR_UNSUPPORTED;
+        if (d_out[m] < 1) return LITHE_ERR_SHAPE;
+        if ((d_out[m] * rank) % kBlock) return LITHE_ERR_ALIGN;
+        if (!y[m]) return LITHE_ERR_NULL;
+        if ((uintptr_t)y[m] & (uintptr_t)(ybytes - 1)) return LITHE_ERR_ALIGN;
+        rc = check_indexed(&f[m], rank, d_in, d_out[m]);
+        if (rc) return rc;
+        // one shrink reads every module's A: one index source and one A value table
+        const lithe_index_src &s0 = f[0].a_idx, &sm = f[m].a_idx;
+        if (sm.base != s0.base || sm.kind != s0.kind || sm.num_levels != s0.num_levels ||
+            sm.slot_stride != s0.slot_stride || sm.level_stride != s0.level_stride || sm.n_slots != s0.n_slots)
+            return LITHE_ERR_UNSUPPORTED;
+        for (int l = 0; l < kMaxLevels; ++l)
+            for (int q = 0; q < 10; ++q)
+                if (f[m].lut_a.value[l][q] != f[0].lut_a.value[l][q]) return LITHE_ERR_UNSUPPORTED;
+        d_out_max = std::max(d_out_max, d_out[m]);
     }
-    return y_dtype == LITHE_DT_BF16 ? dispatch_src<float, __bf16>(p, a, f->kind, st)
-                                    : dispatch_src<float, float>(p, a, f->kind, st);
+    const Plan ps = make_plan(n_batch, seq, d_in, d_out_max, rank, routes->n_route * n_mod, xbytes, false, ybytes);
+    if (workspace_bytes < ps.total) return LITHE_ERR_WORKSPACE;
+
+    LoraArgs a{};
+    a.a_src = make_src(f[0].a_idx);
+    a.a_src.block_off = 0;
+    const int G1 = n_rg * routes->n_route;
+    a.n_slots = f[0].a_idx.n_slots;
+    copy_lut(a.luts.v[0], f[0].lut_a);
+    set_call_fields(a, x, static_cast<char *>(workspace), ps, n_batch, seq, d_in, rank, routes, mid_scale);
+    // Shrink: replicated (one single-module workgroup per tile and module, x shared through the
+    // Infinity Cache) unless LITHE_SHARED_X_STACKED asks for the module-stacked kernel (all
+    // modules' A rows as rank groups of one workgroup).
+    const bool stacked = getenv("LITHE_SHARED_X_STACKED") != nullptr;
+    Plan pshrink = ps;
+    if (stacked) {
+        for (int g = 0; g < kMaxGroups; ++g) a.a_goff[g] = f[std::min(g / G1, n_mod - 1)].a_idx.block_off;
+        a.n_mod_wg = 1;
+    } else {
+        pshrink = make_plan(n_batch, seq, d_in, d_out_max, rank, routes->n_route, xbytes, false, ybytes);
+        for (int g = 0; g < kMaxGroups; ++g) a.a_goff[g] = f[std::min(g, n_mod - 1)].a_idx.block_off;
+        a.n_mod_wg = n_mod;
+    }
+    set_shrink_fields(a, pshrink);
+    a.MR = ps.MR;          // mid rows hold every module's groups
+    a.G1 = G1;
+    a.b_src = make_src(f[0].b_idx);
+    set_module_fields(a, y[0], d_out[0], accumulate, out_scale[0], nullptr);
+    hipStream_t st = (hipStream_t)stream;
+    const int src = src_of(a, LITHE_FACTOR_INDEXED);
+    launch_typed(true, x_dtype, y_dtype, pshrink, a, src, st);
+    for (int m = 0; m < n_mod; ++m) {
+        const Plan pe = make_plan(n_batch, seq, d_in, d_out[m], rank, routes->n_route, xbytes, false, ybytes);
+        LoraArgs e = a;
+        e.b_src = make_src(f[m].b_idx);
+        e.n_slots = std::min(f[m].a_idx.n_slots, f[m].b_idx.n_slots);
+        copy_lut(e.luts.v[1], f[m].lut_b);
+        set_module_fields(e, y[m], d_out[m], accumulate, out_scale[m], nullptr);
+        e.G = pe.G;            // this module's groups; mid rows keep the shrink's width
+        e.mid_goff = m * G1;
+        set_expand_fields(e, pe);
+        launch_typed(false, x_dtype, y_dtype, pe, e, src_of(e, LITHE_FACTOR_INDEXED), st);
+    }
+    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
 }
 
 extern "C" int32_t lithe_workspace_errors(const void *workspace, int32_t *flags, int32_t clear, void *stream) {

@@ -70,6 +70,8 @@ SIGNATURES = {
     "lithe_lora_delta": ([_P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _I32, _I32,
                           ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _F32, _P,
                           _P, _I64, _P], _I32),
+    "lithe_lora_delta_shared_x": ([_P, _I32, _I64, _I64, _I64, _I32, _P, _I32, _P, _I32, _I32,
+                                   ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _P, _P, _I64, _P], _I32),
     "lithe_workspace_errors": ([_P, _P, _I32, _P], _I32),
     "lithe_decode_stacked": ([ctypes.POINTER(IndexSrc), _P, _I32, _I64, _I32, _P, _P, ctypes.POINTER(Lut),
                               ctypes.POINTER(Lut), _P, _I32, _P, _P], _I32),

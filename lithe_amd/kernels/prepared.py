@@ -93,3 +93,61 @@ def prepare_dense(x: torch.Tensor, y: torch.Tensor, a: torch.Tensor, b: torch.Te
     sl = slots.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
     return PreparedDelta(x, y, rank=rank, factors=f, route=_delta.routes(sl), accumulate=accumulate,
                          workspace=workspace, out_scale=scaling, keep=(sl, a, b))
+
+
+class PreparedSharedX:
+    """y_m <- y_m + delta_m(x) for modules that read one input (``lithe_lora_delta_shared_x``):
+    one shrink over x for all of them, then one expand per module."""
+
+    def __init__(self, x: torch.Tensor, ys: Sequence[torch.Tensor], factors: Sequence[_hip.Factors],
+                 route: _hip.Routes, rank: int, out_scales: Sequence[float], workspace: torch.Tensor,
+                 accumulate: bool = True, keep: Sequence = ()):
+        _hip.require_gpu(x, workspace, *ys)
+        if x.dim() != 3 or not x.is_contiguous() or any(y.dim() != 3 or not y.is_contiguous() for y in ys):
+            raise ValueError("x and every y must be contiguous (B, M, D) tensors")
+        n = len(ys)
+        if not (n == len(factors) == len(out_scales)) or n < 1:
+            raise ValueError("one factor set and one scale per output")
+        if any(y.shape[:2] != x.shape[:2] or y.dtype != ys[0].dtype for y in ys):
+            raise ValueError("every y must be (B, M, d_out) like x, in one dtype")
+        need = workspace_bytes(tuple(x.shape), max(y.shape[2] for y in ys), rank, route.n_route * n, x.dtype)
+        if workspace.numel() < need:
+            raise ValueError(f"workspace holds {workspace.numel()} bytes, the call needs {need}")
+        self.x, self.ys, self.workspace = x, list(ys), workspace
+        self._f = (_hip.Factors * n)(*factors)
+        self._y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+        self._d = (ctypes.c_int64 * n)(*[y.shape[2] for y in ys])
+        self._s = (ctypes.c_float * n)(*[float(v) for v in out_scales])
+        self._keep: List = [route, *keep]
+        self._lib = _hip.load()
+        b, m, d_in = x.shape
+        self._args = (_hip.ptr(x), _hip.dtype_code(x.dtype), b, m, d_in, n, self._y, _hip.dtype_code(ys[0].dtype),
+                      self._d, int(bool(accumulate)), int(rank), self._f, ctypes.byref(route), None, self._s,
+                      _hip.ptr(workspace), workspace.numel())
+        self.tokens = b * m
+        self.d_in = d_in
+
+    def algorithmic_bytes(self) -> int:
+        """x read once + every y read and written."""
+        return self.tokens * (self.d_in * self.x.element_size() + sum(2 * y.shape[2] * y.element_size() for y in self.ys))
+
+    def __call__(self, stream: Optional[ctypes.c_void_p] = None) -> None:
+        rc = self._lib.lithe_lora_delta_shared_x(*self._args,
+                                                 stream if stream is not None else _hip.stream_of(self.x.device))
+        if rc:
+            _hip.check(rc, "lithe_lora_delta_shared_x")
+
+
+def prepare_packed_shared_x(x: torch.Tensor, ys: Sequence[torch.Tensor], bank_words: torch.Tensor,
+                            offsets: Sequence[Tuple[int, int]], num_levels: int,
+                            pools: Tuple[torch.Tensor, torch.Tensor], slots: torch.Tensor, rank: int, scaling: float,
+                            workspace: torch.Tensor, accumulate: bool = True) -> PreparedSharedX:
+    """Prepared index-resident deltas of the modules at ``offsets`` [(a_off, b_off)] of a packed
+    bank, all reading ``x`` (e.g. to_q / to_k / to_v of one attention block)."""
+    lut_a = _hip.lut_from_pools(pools[0], x.dtype)
+    lut_b = _hip.lut_from_pools(pools[1], x.dtype)
+    fs = [_delta.indexed_factors(_delta.packed_source(bank_words, num_levels, ao),
+                                 _delta.packed_source(bank_words, num_levels, bo), lut_a, lut_b) for ao, bo in offsets]
+    sl = slots.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
+    return PreparedSharedX(x, ys, fs, _delta.routes(sl), rank, [scaling] * len(ys), workspace, accumulate,
+                           keep=(sl, bank_words))
