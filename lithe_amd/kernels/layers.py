@@ -22,6 +22,7 @@ import torch
 from torch import nn
 
 from . import _delta, _hip
+from . import ops as _ops  # noqa: F401  (registers the lithe_amd:: operators)
 from .sgmv import lora_delta_dense, per_sample_lora_delta
 
 Factor = Tuple[torch.Tensor, torch.Tensor, float]
@@ -48,6 +49,15 @@ class PerSampleLoRALinear(nn.Module):
         self.factors = list(factors)
         self.per_sample = per_sample
         self._stacked = None
+
+    def set_stacked(self, a: torch.Tensor, b: torch.Tensor, scales: torch.Tensor) -> None:
+        """Install already stacked factors a (n, r, d_in), b (n, d_out, r) and scales (n,) -- e.g.
+        views from ``PackedBank.decode_stacked`` -- without the stacking copy."""
+        if a.dim() != 3 or b.dim() != 3 or a.shape[0] != b.shape[0] or scales.numel() != a.shape[0]:
+            raise ValueError("stacked factors must be (n, r, d_in), (n, d_out, r) with n scales")
+        self.factors = [(a[i], b[i], float(scales[i])) for i in range(a.shape[0])]
+        self.per_sample = True
+        self._stacked = (a.contiguous(), b.contiguous(), scales.to(device=a.device, dtype=torch.float32))
 
     def clear(self) -> None:
         self.set_factors([], per_sample=False)
@@ -162,8 +172,15 @@ class IndexLoRALinear(nn.Module):
         if not out3.is_contiguous():
             out3 = out3.contiguous()
             out = out3.squeeze(1) if squeeze else out3
-        _delta.lora_delta(x3.contiguous(), out3, rank=self.rank, factors=self._factors(x.dtype),
-                          route=_delta.routes(slots), accumulate=True, out_scale=self.scaling)
+        # through the torch.library ops (lithe_amd/kernels/ops.py): one opaque in-place op for
+        # torch.compile / FX
+        if self._bank is not None:
+            bank, a_off, b_off = self._bank
+            torch.ops.lithe_amd.bank_lora_delta_(x3.contiguous(), out3, bank.words, a_off, b_off, self.pool_a,
+                                                 self.pool_b, slots, self.rank, self.scaling)
+        else:
+            torch.ops.lithe_amd.index_lora_delta_(x3.contiguous(), out3, self.idx_a, self.idx_b, self.pool_a,
+                                                  self.pool_b, slots, self.rank, self.scaling)
         return out
 
 

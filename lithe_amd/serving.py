@@ -1,0 +1,203 @@
+"""Wrapping a transformer's linears for multi-adapter serving (``serving/_common.py:276-311``).
+
+* ``select_paths`` / ``wrap_index`` / ``set_assign`` keep the reference's names and
+  semantics: every target linear becomes an ``IndexLoRALinear`` holding the index slots of
+  all adapters as per-layer int32 stacks, and ``set_assign`` routes the samples.
+* ``wrap_bank`` is the resident-bank form: every target linear reads its slots straight
+  from one ``PackedBank`` (no per-layer copies; a cold swap into the bank is visible to
+  every layer at once). With ``fuse_shared_inputs`` the projections that read one input
+  (``to_q`` / ``to_k`` / ``to_v``, ``add_q_proj`` / ``add_k_proj`` / ``add_v_proj``) share
+  one shrink over x (``lithe_lora_delta_shared_x``).
+* ``wrap_decoded`` / ``install_per_sample`` / ``install_single`` are the decoded-mode
+  counterparts (``serving/_common.py:268-281``), and ``install_decoded_bank`` installs the
+  stacked factors of ``PackedBank.decode_stacked`` without per-module copies.
+
+Model loading and rendering (diffusers pipelines) are not part of this package.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+import torch
+from torch import nn
+
+from .kernels import _delta, _hip
+from .kernels.bank import PackedBank
+from .kernels.layers import IndexLoRALinear, PerSampleLoRALinear, wrap_linears
+from .kernels.prepared import workspace_bytes
+from .module import FLUX_TARGET_MODULES
+from . import codebook as cb
+
+SHARED_INPUT_GROUPS = (("attn.to_q", "attn.to_k", "attn.to_v"),
+                       ("attn.add_q_proj", "attn.add_k_proj", "attn.add_v_proj"))
+
+
+def select_paths(paths: Sequence[str], module_set: str = "all") -> List[str]:
+    """``all``: every path; ``attn-ff``: the attention / feed-forward linears of
+    ``FLUX_TARGET_MODULES`` (``serving/_common.py:284-291``)."""
+    if module_set == "all":
+        return list(paths)
+    if module_set == "attn-ff":
+        return [p for p in paths if any(p.endswith(s) for s in FLUX_TARGET_MODULES)]
+    raise ValueError(f"unknown module set {module_set!r}")
+
+
+def wrap_index(model: nn.Module, ads, device, dtype: torch.dtype = torch.bfloat16,
+               module_set: str = "all") -> Dict[str, IndexLoRALinear]:
+    """Index-resident wrappers holding the index slots of all ``ads`` (``serving/_common.py:294-306``):
+    per layer, (n_adapters, L, n_blocks) int32 stacks of A and B and the pools in ``dtype``."""
+    pa, pb = (p.to(device=device, dtype=dtype) for p in cb.twin_pools(ads[0].block_size, ads[0].n_bits,
+                                                                     ads[0].sigma_a, ads[0].sigma_b))
+    scale = float(ads[0].alpha) / ads[0].rank
+    paths = [m["name"] for m in ads[0].modules]
+
+    def factory(path, lin):
+        ia = torch.stack([torch.from_numpy(np.asarray(ad.indices[path]["A"]).astype(np.int32)) for ad in ads])
+        ib = torch.stack([torch.from_numpy(np.asarray(ad.indices[path]["B"]).astype(np.int32)) for ad in ads])
+        return IndexLoRALinear(lin, ia.to(device), ib.to(device), pa, pb, ads[0].rank, scale)
+
+    return wrap_linears(model, select_paths(paths, module_set), factory)
+
+
+def set_assign(wrapped: Dict[str, nn.Module], assign: Optional[torch.Tensor]) -> None:
+    """Route sample i of every wrapped linear to slot ``assign[i]`` (``serving/_common.py:309-311``)."""
+    for mod in wrapped.values():
+        mod.assign = assign
+
+
+class SharedInputGroup:
+    """Bank-backed layers whose linears read the same input (the q / k / v projections).
+
+    The first member called with an input computes every member's base output, adds all
+    their deltas with one shrink over x (``lithe_lora_delta_shared_x``), returns its own and
+    keeps the others until their members are called with the same input (same storage,
+    shape, dtype and version counter). A member called with another input falls back to
+    computing the group for that input, so results never depend on the call order.
+    """
+
+    def __init__(self, layers: Sequence[IndexLoRALinear]):
+        if len(layers) < 2 or any(l._bank is None for l in layers):
+            raise ValueError("a shared-input group needs two or more bank-backed layers")
+        bank = layers[0]._bank[0]
+        if any(l._bank[0] is not bank or l.rank != layers[0].rank or l.base.in_features != layers[0].base.in_features
+               for l in layers):
+            raise ValueError("grouped layers must share one bank, rank and input width")
+        self.layers = list(layers)
+        self._key = None
+        self._pending: List[Optional[torch.Tensor]] = [None] * len(layers)
+
+    def _compute(self, x: torch.Tensor) -> List[torch.Tensor]:
+        lead = self.layers[0]
+        outs = [l.base(x) for l in self.layers]
+        squeeze = x.dim() == 2
+        x3 = (x.unsqueeze(1) if squeeze else x).contiguous()
+        o3 = [(o.unsqueeze(1) if squeeze else o) for o in outs]
+        o3 = [o if o.is_contiguous() else o.contiguous() for o in o3]
+        bsz = x3.shape[0]
+        slots = (torch.zeros((bsz, 1), dtype=torch.int32, device=x.device) if lead.assign is None
+                 else lead.assign.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous())
+        fs = [l._factors(x.dtype) for l in self.layers]
+        n = len(self.layers)
+        lib = _hip.load()
+        need = workspace_bytes(tuple(x3.shape), max(o.shape[2] for o in o3), lead.rank, n, x.dtype)
+        ws = _hip.workspace(x.device, need)
+        fa = (_hip.Factors * n)(*fs)
+        ya = (ctypes.c_void_p * n)(*[o.data_ptr() for o in o3])
+        da = (ctypes.c_int64 * n)(*[o.shape[2] for o in o3])
+        sa = (ctypes.c_float * n)(*[l.scaling for l in self.layers])
+        route = _delta.routes(slots)
+        rc = lib.lithe_lora_delta_shared_x(_hip.ptr(x3), _hip.dtype_code(x.dtype), bsz, x3.shape[1], x3.shape[2], n,
+                                           ya, _hip.dtype_code(o3[0].dtype), da, 1, lead.rank, fa,
+                                           ctypes.byref(route), None, sa, _hip.ptr(ws), ws.numel(),
+                                           _hip.stream_of(x.device))
+        _hip.check(rc, "lithe_lora_delta_shared_x")
+        return [o.squeeze(1) if squeeze else o for o in o3]
+
+    def output(self, i: int, x: torch.Tensor) -> torch.Tensor:
+        key = (x.data_ptr(), tuple(x.shape), x.dtype, x._version)
+        if key == self._key and self._pending[i] is not None:
+            out, self._pending[i] = self._pending[i], None
+            return out
+        outs = self._compute(x)
+        self._key = key
+        self._pending = [o if j != i else None for j, o in enumerate(outs)]
+        return outs[i]
+
+
+class SharedInputMember(nn.Module):
+    """Stands in for one layer of a ``SharedInputGroup`` (same ``base``, ``assign`` and slots)."""
+
+    def __init__(self, group: SharedInputGroup, index: int):
+        super().__init__()
+        self.layer = group.layers[index]
+        self._group = group
+        self._index = index
+
+    @property
+    def base(self) -> nn.Linear:
+        return self.layer.base
+
+    @property
+    def assign(self):
+        return self.layer.assign
+
+    @assign.setter
+    def assign(self, value):
+        self.layer.assign = value
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._group.output(self._index, x)
+
+
+def wrap_bank(model: nn.Module, bank: PackedBank, module_set: str = "all", dtype: Optional[torch.dtype] = None,
+              fuse_shared_inputs: bool = False) -> Dict[str, nn.Module]:
+    """Bank-backed index-resident wrappers for every linear named in the bank's layout."""
+    paths = select_paths(bank.layout.names, module_set)
+    wrapped = wrap_linears(model, paths, lambda p, lin: IndexLoRALinear.from_bank(lin, bank, p, dtype))
+    if fuse_shared_inputs:
+        for path in list(wrapped):
+            for names in SHARED_INPUT_GROUPS:
+                if not path.endswith(names[0]):
+                    continue
+                prefix = path[: -len(names[0])]
+                members = [prefix + n for n in names]
+                if not all(m in wrapped and isinstance(wrapped[m], IndexLoRALinear) for m in members):
+                    continue
+                group = SharedInputGroup([wrapped[m] for m in members])
+                for i, m in enumerate(members):
+                    stand_in = SharedInputMember(group, i)
+                    parent_name, _, child = m.rpartition(".")
+                    parent = model.get_submodule(parent_name) if parent_name else model
+                    setattr(parent, child, stand_in)
+                    wrapped[m] = stand_in
+    return wrapped
+
+
+def wrap_decoded(model: nn.Module, paths: Sequence[str], kernel: str = "sgmv") -> Dict[str, PerSampleLoRALinear]:
+    """Decoded-mode wrappers (``serving/_common.py:268-269``)."""
+    return wrap_linears(model, paths, lambda p, lin: PerSampleLoRALinear(lin, kernel))
+
+
+def install_per_sample(wrapped: Dict[str, PerSampleLoRALinear], decoded: Sequence[Dict]) -> None:
+    """Point every wrapped linear at the factors of ``decoded[i]`` for slot i (``serving/_common.py:272-275``)."""
+    for path, mod in wrapped.items():
+        mod.set_factors([d[path] for d in decoded], per_sample=True)
+
+
+def install_single(wrapped: Dict[str, PerSampleLoRALinear], decoded: Dict) -> None:
+    """One adapter for every sample (``serving/_common.py:278-280``)."""
+    for path, mod in wrapped.items():
+        mod.set_factors([decoded[path]], per_sample=False)
+
+
+def install_decoded_bank(wrapped: Dict[str, PerSampleLoRALinear], bank: PackedBank, slots) -> Dict:
+    """Decode-on-swap: the selected bank slots decoded in one launch, installed as every
+    layer's stacked factors (factor pair i = ``slots[i]``; set ``assign`` to pick pairs)."""
+    st = bank.decode_stacked(slots)
+    n = len(list(slots))
+    for path, mod in wrapped.items():
+        a, b = st[path]
+        mod.set_stacked(a, b, torch.full((n,), bank.layout.scaling, dtype=torch.float32, device=a.device))
+    return st

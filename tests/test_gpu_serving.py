@@ -1,0 +1,101 @@
+"""GPU checks of the serving helpers on a FLUX-shaped toy transformer:
+
+* ``wrap_index`` (per-layer int32 index stacks, the reference's serving/_common.py:294-306)
+  and ``wrap_bank`` (slots read from the packed bank) give bit-equal outputs (same factors,
+  same kernels and plan);
+* the shared-input groups (q / k / v through ``lithe_lora_delta_shared_x``) match the unfused
+  model at the bf16 delta tolerance (the shrink plans split K differently);
+* decoded mode through ``install_decoded_bank`` matches the index-resident model at that
+  tolerance (decoded factors are summed from fp32 pools, the fused path's from bf16 pools);
+* ``torch.compile`` traces the wrapped model without graph breaks (the delta is one
+  ``lithe_amd::`` op) and its result equals eager bit for bit.
+"""
+import copy
+
+import pytest
+import torch
+
+from lithe_amd import serving
+from lithe_amd.kernels import PackedBank
+
+from helpers import random_adapter, rel, to_np
+from toy_flux import ToyFlux, target_modules
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(seed=0, n_ad=4):
+    torch.manual_seed(seed)
+    model = ToyFlux().cuda().bfloat16()
+    mods = target_modules(model)
+    ads = [random_adapter(mods, rank=16, seed=200 + s) for s in range(n_ad)]
+    bank, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bank.add(w)
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    h = torch.randn(3, 64, 256, device="cuda", generator=g).bfloat16()
+    c = torch.randn(3, 24, 256, device="cuda", generator=g).bfloat16()
+    return model, ads, bank, h, c
+
+
+def test_wrap_index_equals_wrap_bank():
+    model, ads, bank, h, c = _setup()
+    m1, m2 = copy.deepcopy(model), copy.deepcopy(model)
+    w1 = serving.wrap_index(m1, ads, "cuda")
+    w2 = serving.wrap_bank(m2, bank)
+    assign = torch.tensor([2, 0, 3], dtype=torch.int32, device="cuda")
+    serving.set_assign(w1, assign)
+    serving.set_assign(w2, assign)
+    with torch.no_grad():
+        base = model(h, c)
+        o1, o2 = m1(h, c), m2(h, c)
+    assert torch.equal(o1, o2)
+    assert rel(to_np(o1), to_np(base)) > 1e-3          # the adapters changed the output
+
+
+def test_shared_input_groups_match_unfused():
+    model, ads, bank, h, c = _setup(1)
+    m1, m2 = copy.deepcopy(model), copy.deepcopy(model)
+    w1 = serving.wrap_bank(m1, bank)
+    w2 = serving.wrap_bank(m2, bank, fuse_shared_inputs=True)
+    assign = torch.tensor([1, 3, 1], dtype=torch.int32, device="cuda")
+    serving.set_assign(w1, assign)
+    serving.set_assign(w2, assign)
+    with torch.no_grad():
+        o1, o2 = m1(h, c), m2(h, c)
+        o3 = m2(h, c)                                  # second pass: no stale group state
+    assert rel(to_np(o2), to_np(o1)) < 2e-3
+    assert torch.equal(o2, o3)
+    # a member called with another input than its group's pending one recomputes
+    q = m2.transformer_blocks[0].attn.to_q(h)
+    k_other = m2.transformer_blocks[0].attn.to_k(h + 1)
+    with torch.no_grad():
+        k_ref = m1.transformer_blocks[0].attn.to_k(h + 1)
+    assert rel(to_np(k_other), to_np(k_ref)) < 2e-3 and q.shape == h.shape
+
+
+def test_decoded_bank_mode_matches_index_resident():
+    model, ads, bank, h, c = _setup(2)
+    m1, m2 = copy.deepcopy(model), copy.deepcopy(model)
+    w1 = serving.wrap_bank(m1, bank)
+    w2 = serving.wrap_decoded(m2, [n for n, _, _ in target_modules(model)])
+    sel = [3, 0]
+    serving.install_decoded_bank(w2, bank, sel)
+    serving.set_assign(w1, torch.tensor([3, 0, 3], dtype=torch.int32, device="cuda"))
+    serving.set_assign(w2, torch.tensor([0, 1, 0], dtype=torch.int32, device="cuda"))   # pairs of sel
+    with torch.no_grad():
+        o1, o2 = m1(h, c), m2(h, c)
+    assert rel(to_np(o2), to_np(o1)) < 1e-2
+
+
+def test_torch_compile_traces_the_lithe_ops():
+    model, ads, bank, h, c = _setup(3)
+    w = serving.wrap_bank(model, bank)
+    serving.set_assign(w, torch.tensor([0, 2, 1], dtype=torch.int32, device="cuda"))
+    torch._dynamo.reset()
+    with torch.no_grad():
+        eager = model(h, c)
+        explain = torch._dynamo.explain(model)(h, c)
+        compiled = torch.compile(model, backend="aot_eager", fullgraph=True)(h, c)
+    assert explain.graph_break_count == 0
+    assert torch.equal(compiled, eager)

@@ -1,0 +1,46 @@
+"""CPU checks of the serving helpers: target selection, bank-backed wrapping of a FLUX-shaped
+model (with and without shared-input groups) and routing propagation. No kernel runs here."""
+import pytest
+import torch
+
+from lithe_amd import serving
+from lithe_amd.kernels import IndexLoRALinear, PackedBank, PackedLayout
+
+from toy_flux import ToyFlux, target_modules
+
+
+def _bank(model):
+    mods = target_modules(model)
+    lay = PackedLayout.from_modules([{"name": n, "shape_a": [16, di], "shape_b": [do, 16]} for n, di, do in mods])
+    return PackedBank(lay, "cpu", capacity=2)
+
+
+def test_target_selection_counts():
+    model = ToyFlux(n_double=2, n_single=3)
+    paths = [n for n, _, _ in target_modules(model)]
+    assert len(paths) == 2 * 12 + 3 * 3          # the 19 x 12 + 38 x 3 = 342 rule of FLUX.1-dev, scaled down
+    extra = paths + ["single_transformer_blocks.0.proj_mlp", "norm_out.linear"]
+    assert serving.select_paths(extra, "attn-ff") == paths
+    assert serving.select_paths(extra) == extra
+    with pytest.raises(ValueError):
+        serving.select_paths(extra, "nope")
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_wrap_bank_structure_and_assign(fuse):
+    model = ToyFlux()
+    bank = _bank(model)
+    wrapped = serving.wrap_bank(model, bank, fuse_shared_inputs=fuse)
+    assert len(wrapped) == len(target_modules(ToyFlux()))
+    members = [p for p, m in wrapped.items() if isinstance(m, serving.SharedInputMember)]
+    if fuse:
+        # 2 double blocks x (img q/k/v + txt q/k/v) + 2 single blocks x q/k/v
+        assert len(members) == 2 * 6 + 2 * 3
+        assert model.transformer_blocks[0].attn.to_k is wrapped["transformer_blocks.0.attn.to_k"]
+    else:
+        assert not members and all(isinstance(m, IndexLoRALinear) for m in wrapped.values())
+    assign = torch.tensor([1, 0, 1], dtype=torch.int32)
+    serving.set_assign(wrapped, assign)
+    assert all(m.assign is assign for m in wrapped.values())
+    lead = model.single_transformer_blocks[1].attn.to_q
+    assert (lead.layer if fuse else lead).assign is assign

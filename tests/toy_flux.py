@@ -1,0 +1,85 @@
+"""A FLUX-shaped toy transformer (module paths of diffusers' FluxTransformer2DModel, tiny widths)
+for the serving tests: double blocks with image / text attention projections and feed-forwards,
+single blocks with q / k / v."""
+import torch
+from torch import nn
+
+
+class _Proj(nn.Module):
+    def __init__(self, d_in, d_out):
+        super().__init__()
+        self.proj = nn.Linear(d_in, d_out)
+
+
+class _Attn(nn.Module):
+    def __init__(self, d, context=True):
+        super().__init__()
+        self.to_q, self.to_k, self.to_v = nn.Linear(d, d), nn.Linear(d, d), nn.Linear(d, d)
+        if context:     # single-block attention is projection-only (no to_out), as in FLUX
+            self.to_out = nn.ModuleList([nn.Linear(d, d)])
+            self.add_q_proj, self.add_k_proj, self.add_v_proj = nn.Linear(d, d), nn.Linear(d, d), nn.Linear(d, d)
+            self.to_add_out = nn.Linear(d, d)
+
+
+class _FF(nn.Module):
+    def __init__(self, d, ff):
+        super().__init__()
+        self.net = nn.ModuleList([_Proj(d, ff), nn.GELU(), nn.Linear(ff, d)])
+
+    def forward(self, x):
+        return self.net[2](self.net[1](self.net[0].proj(x)))
+
+
+class DoubleBlock(nn.Module):
+    def __init__(self, d, ff):
+        super().__init__()
+        self.attn = _Attn(d)
+        self.ff = _FF(d, ff)
+        self.ff_context = _FF(d, ff)
+
+    def forward(self, h, c):
+        a = self.attn
+        q, k, v = a.to_q(h), a.to_k(h), a.to_v(h)
+        h = h + a.to_out[0](q * torch.sigmoid(k) + v)
+        cq, ck, cv = a.add_q_proj(c), a.add_k_proj(c), a.add_v_proj(c)
+        c = c + a.to_add_out(cq * torch.sigmoid(ck) + cv)
+        return h + self.ff(h), c + self.ff_context(c)
+
+
+class SingleBlock(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.attn = _Attn(d, context=False)
+
+    def forward(self, h):
+        a = self.attn
+        return h + a.to_q(h) * torch.sigmoid(a.to_k(h)) + a.to_v(h)
+
+
+class ToyFlux(nn.Module):
+    def __init__(self, d=256, ff=512, n_double=2, n_single=2):
+        super().__init__()
+        self.transformer_blocks = nn.ModuleList([DoubleBlock(d, ff) for _ in range(n_double)])
+        self.single_transformer_blocks = nn.ModuleList([SingleBlock(d) for _ in range(n_single)])
+
+    def forward(self, h, c):
+        for b in self.transformer_blocks:
+            h, c = b(h, c)
+        h = torch.cat([c, h], dim=1)
+        for b in self.single_transformer_blocks:
+            h = b(h)
+        return h
+
+
+TARGETS = ("attn.to_q", "attn.to_k", "attn.to_v", "attn.to_out.0", "attn.add_q_proj", "attn.add_k_proj",
+           "attn.add_v_proj", "attn.to_add_out", "ff.net.0.proj", "ff.net.2", "ff_context.net.0.proj",
+           "ff_context.net.2")
+
+
+def target_modules(model: nn.Module):
+    """(path, d_in, d_out) of the model's FLUX target linears, in model order."""
+    out = []
+    for name, mod in model.named_modules():
+        if isinstance(mod, nn.Linear) and any(name.endswith(t) for t in TARGETS):
+            out.append((name, mod.in_features, mod.out_features))
+    return out
