@@ -10,7 +10,7 @@ inside the kernels. Inputs are synthetic (x, y ~ N(0, 1); uniformly random
 9-bit fields) and already resident in HBM; x / y buffers rotate so the 256 MB
 Infinity Cache cannot serve a module from a previous module's data.
 
-    python bench.py [--steps K] [--warmup W] [--config flux342|decoded|ffn|hb|decode|ingest] [--rank 16|64]
+    python bench.py [--steps K] [--warmup W] [--config flux342|qkv|decoded|ffn|hb|decode|ingest|encode] [--rank 16|64]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -483,13 +483,95 @@ def run_ingest(args):
     print(json.dumps(line), flush=True)
 
 
+def run_encode(args):
+    """GPU re-quantisation: a dense rank-16 adapter of the 342 FLUX linears -> packed bank slot."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from lithe_amd.kernels import PackedBank, PackedLayout, _hip
+    dev = torch.device("cuda:0")
+    mods = flux_modules(4096, 512)
+    layout = PackedLayout.from_modules(
+        [{"name": n, "shape_a": [RANK, di], "shape_b": [do, RANK]} for n, di, do, _ in mods],
+        num_levels=3, block_size=64, scaling=1.0)
+    bank = PackedBank(layout, dev, capacity=4)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    # synthetic dense factors at the codebook's scales (A ~ 0.06 N(0,1), B ~ 0.0025 N(0,1))
+    factors = {n: (0.06 * torch.randn(RANK, di, device=dev, generator=gen),
+                   0.0025 * torch.randn(do, RANK, device=dev, generator=gen)) for n, di, do, _ in mods}
+    for _ in range(args.warmup):
+        bank.encode_factors(factors, slot=0 if bank.num_slots else None)
+    torch.cuda.synchronize()
+    n = max(5, args.steps)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        bank.encode_factors(factors, slot=0)
+    torch.cuda.synchronize()
+    e2e_ms = (time.perf_counter() - t0) / n * 1e3
+    # the encode kernel alone over the adapter's blocks (residency order, both pools)
+    blocks = torch.randn(layout.total_blocks, 64, device=dev, generator=gen) * 0.01
+    idx = torch.empty(layout.total_blocks * 3, dtype=torch.int16, device=dev)
+    lut_a = _hip.lut_from_pools(bank.pool_a, torch.float32)
+    lut_b = _hip.lut_from_pools(bank.pool_b, torch.float32)
+    lib = _hip.load()
+    sides = layout.sides_on(dev)
+
+    def launch():
+        lib.lithe_encode(_hip.ptr(blocks), layout.total_blocks, _hip.ptr(sides), ctypes.byref(lut_a),
+                         ctypes.byref(lut_b), _hip.ptr(idx), _hip.DT_I16, 1, 3, None, _hip.stream_of(dev))
+
+    for _ in range(3):
+        launch()
+    cs = torch.cuda.current_stream()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(cs)
+    reps = 50
+    for _ in range(reps):
+        launch()
+    e.record(cs)
+    torch.cuda.synchronize()
+    k_ms = s.elapsed_time(e) / reps
+    k_bytes = layout.total_blocks * (64 * 4 + 3 * 2 + 1)      # fp32 block in, 3 int16 indices + side byte
+    cpu = None
+    if not args.no_cpu:
+        from oracle import codebook as ocb
+        from oracle import search as osr
+        pa, _ = ocb.twin_pools()
+        sample = blocks[:100_000].cpu().numpy()
+        t0, k = time.perf_counter(), 0
+        while k < 1 or time.perf_counter() - t0 < 10.0:
+            osr.rvq_encode_blocks(sample, pa)
+            k += 1
+        per_block = (time.perf_counter() - t0) / (k * sample.shape[0])
+        cpu = {"value": round(per_block * layout.total_blocks * 1e3, 1), "unit": "ms per adapter", "cores": 1,
+               "kind": "port", "sample": f"oracle greedy encode (numpy, float64 projections) of {k} x 100,000 blocks, "
+                                       f"scaled to the adapter's {layout.total_blocks} blocks"}
+    line = {
+        "metric": "GPU re-quantisation latency: dense rank-16 adapter (342 FLUX linears) -> packed bank slot",
+        "value": round(e2e_ms, 3), "unit": "ms", "n_gpus": 1, "steps": n, "warmup": args.warmup,
+        "ms_per_step": round(e2e_ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"closed-form greedy 3-level encode of {layout.total_blocks} blocks (fp32 factors "
+                               f"blockified in layout order) + 9-bit pack into a slot", "rank": RANK,
+                   "blocks": layout.total_blocks},
+        "roofline": {"kernel": "encode_kernel (lithe_encode)", "bound": "hbm",
+                     "achieved": round(k_bytes / (k_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(k_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": k_bytes, "mean_launch_ms": round(k_ms, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="flux342",
-                    choices=["flux342", "qkv", "decoded", "ffn", "hb", "decode", "ingest"])
+                    choices=["flux342", "qkv", "decoded", "ffn", "hb", "decode", "ingest", "encode"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -513,6 +595,9 @@ def main():
         return
     if args.config == "ingest":
         run_ingest(args)
+        return
+    if args.config == "encode":
+        run_encode(args)
         return
     rng = np.random.default_rng(1234)
     if args.config in ("flux342", "decoded", "qkv"):

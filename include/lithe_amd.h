@@ -146,6 +146,25 @@ int32_t lithe_decode_stacked(const lithe_index_src *src, const int32_t *slots, i
                              const int8_t *sides, const lithe_lut *lut_a, const lithe_lut *lut_b,
                              void *out, int32_t out_dtype, int32_t *err_flag, void *stream);
 
+/* ---------------------------------------------------------------- encode (nearest-codeword search) */
+/* Greedy L-level encode of n 64-value fp32 blocks against the twin codebook, L = lut_a->num_levels:
+ * at level l, bit q of the index is [<r, U[:, q]> > 0] for the residual r and the nine
+ * Sylvester-Hadamard columns U[t, q] = (-1)^popcount(t & q) (all codewords of a level have one
+ * norm, so this is the nearest codeword); the codeword value[l][popcount((k ^ m_t) & 511)] is
+ * added to the reconstruction and subtracted from the residual in fp32. sides[i] = 1 (sides
+ * nullable) encodes block i with lut_b, else lut_a. Index l of block i is written to
+ * idx[l * idx_level_stride + i * idx_block_stride] (dtype I16, I32 or I64): (L, n) level-major
+ * (block stride 1, level stride >= n: a .lithe factor matrix) or (n, L) block-major (level
+ * stride 1, block stride >= L: the residency order of a slot). recon (nullable, 16-byte
+ * aligned) receives the (n, 64) fp32 reconstruction. The fp32 projections are summed in a fixed
+ * order that differs from a BLAS matmul, so a projection within rounding of zero may take the
+ * other sign.
+ * Replaces _lattice_search_kernel / lattice_search / rvq_encode_blocks_fast
+ * (lithe/kernels/search.py:27-99) and quant.rvq_encode_blocks (lithe/quant.py:46-71). */
+int32_t lithe_encode(const float *blocks, int64_t n, const int8_t *sides, const lithe_lut *lut_a,
+                     const lithe_lut *lut_b, void *idx, int32_t idx_dtype, int64_t idx_level_stride,
+                     int64_t idx_block_stride, float *recon, void *stream);
+
 /* ---------------------------------------------------------------- per-sample LoRA delta */
 /* Where the factors of the delta come from. */
 #define LITHE_FACTOR_INDEXED 1   /* decoded in-kernel from index sources + value tables */

@@ -19,7 +19,7 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJ_DIR = os.path.join(HERE, "_obj")
 LIB_PATH = os.path.join(PKG, "_lib", "liblithe_amd.so")
 
-SOURCES = ["decode.hip", "lora.hip", "ingest.hip", "host.cpp"]
+SOURCES = ["decode.hip", "lora.hip", "ingest.hip", "encode.hip", "host.cpp"]
 ARCH = os.environ.get("LITHE_OFFLOAD_ARCH", "gfx950")
 
 

@@ -75,6 +75,7 @@ SIGNATURES = {
     "lithe_workspace_errors": ([_P, _P, _I32, _P], _I32),
     "lithe_decode_stacked": ([ctypes.POINTER(IndexSrc), _P, _I32, _I64, _I32, _P, _P, ctypes.POINTER(Lut),
                               ctypes.POINTER(Lut), _P, _I32, _P, _P], _I32),
+    "lithe_encode": ([_P, _I64, _P, ctypes.POINTER(Lut), ctypes.POINTER(Lut), _P, _I32, _I64, _I64, _P, _P], _I32),
     "lithe_ingest_table": ([_I32, _P, _P, _I32, _P], _I32),
     "lithe_ingest_host": ([_P, _I64, _I32, _I32, _P, _P, _I64], _I32),
     "lithe_ingest": ([_P, _I64, _I32, _I32, _P, _P, _I64, _P, _P], _I32),

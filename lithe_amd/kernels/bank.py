@@ -229,6 +229,41 @@ class PackedBank:
         _hip.check(rc, "lithe_pack9")
         return target
 
+    def encode_factors(self, factors: Dict[str, Tuple[torch.Tensor, torch.Tensor]], slot: Optional[int] = None) -> int:
+        """GPU re-quantisation of a dense adapter into a slot: ``factors`` {module: (A (r, d_in),
+        B (d_out, r))} of this layout are blockified (row-major, zero-padded), encoded level by
+        level with the closed-form search against the bank's fp32 pools (``lithe_encode``; A
+        blocks with pool A, B blocks with pool B) straight into the residency order, and packed
+        into the slot (``lithe_pack9``). Replaces ``quant.encode`` per factor +
+        ``pack_adapter`` + ``PackedBank.add`` (``lithe/quant.py:84-88``,
+        ``lithe/kernels/packed.py:136-143``). Returns the slot id."""
+        lay = self.layout
+        bs = lay.block_size
+        blocks = torch.zeros((lay.total_blocks, bs), dtype=torch.float32, device=self.device)
+        for name, sa, sb, ao, bo in zip(lay.names, lay.shapes_a, lay.shapes_b, lay.a_off, lay.b_off):
+            if name not in factors:
+                raise ValueError(f"missing factors of module {name}")
+            a, b = factors[name]
+            if tuple(a.shape) != sa or tuple(b.shape) != sb:
+                raise ValueError(f"{name}: factors {tuple(a.shape)} / {tuple(b.shape)}, layout {sa} / {sb}")
+            for w, off in ((a, ao), (b, bo)):
+                flat = w.detach().reshape(-1).to(device=self.device, dtype=torch.float32)
+                blocks.view(-1)[off * bs: off * bs + flat.numel()].copy_(flat)
+        L = lay.num_levels
+        idx = torch.empty(lay.total_blocks * L, dtype=torch.int16, device=self.device)
+        lut_a = _hip.lut_from_pools(self.pool_a, torch.float32)
+        lut_b = _hip.lut_from_pools(self.pool_b, torch.float32)
+        lib = _hip.load()
+        st = _hip.stream_of(self.device)
+        _hip.check(lib.lithe_encode(_hip.ptr(blocks), lay.total_blocks, _hip.ptr(lay.sides_on(self.device)),
+                                    ctypes.byref(lut_a), ctypes.byref(lut_b), _hip.ptr(idx), _hip.DT_I16, 1, L, None,
+                                    st), "lithe_encode")
+        target = self._target(slot)
+        _, _, err, _ = self._staging(1)
+        _hip.check(lib.lithe_pack9(_hip.ptr(idx), _hip.DT_I16, idx.numel(), _hip.ptr(self._words[target]),
+                                   _hip.ptr(err), st), "lithe_pack9")
+        return target
+
     def ingest_errors(self, clear: bool = True) -> int:
         """Error bits the device ingest recorded since the last clear (synchronises)."""
         st = self._stage

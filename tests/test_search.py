@@ -1,0 +1,54 @@
+"""CPU pins of the oracle's nearest-codeword search and greedy encode (lithe/quant.py:46-71):
+brute force over all 512 codewords, exact round trips of lattice points, and the exact
+per-coordinate error recursion of the nine orthogonal Hadamard directions
+(tests/test_quant.py:17-74 of the reference, restated)."""
+import numpy as np
+
+from oracle import codebook as ocb
+from oracle import decode as odec
+from oracle import search as osr
+
+
+def test_closed_form_equals_brute_force():
+    rng = np.random.default_rng(0)
+    pa, pb = ocb.twin_pools()
+    for pools, scale in ((pa, 0.08), (pb, 0.003)):
+        x = (scale * rng.standard_normal((4096, 64))).astype(np.float32)
+        idx, _ = osr.nearest_index(x)
+        assert np.array_equal(idx, osr.cdist_nearest(x, pools[0]))
+
+
+def test_planted_wrong_hyperplanes_fail_the_pin():
+    rng = np.random.default_rng(1)
+    pa, _ = ocb.twin_pools()
+    x = (0.08 * rng.standard_normal((2048, 64))).astype(np.float32)
+    wrong = ocb.hadamard(64)[:, 1:10].astype(np.float64)        # columns 1..9 instead of 0..8
+    idx, _ = osr.nearest_index(x, wrong)
+    assert (idx != osr.cdist_nearest(x, pa[0])).mean() > 0.5
+
+
+def test_lattice_points_round_trip_exactly():
+    rng = np.random.default_rng(2)
+    _, pb = ocb.twin_pools()
+    true_idx = rng.integers(0, 512, (3, 2048))
+    x = odec.rvq_decode(true_idx, pb)
+    idx, rec, _ = osr.rvq_encode_blocks(x, pb)
+    assert np.array_equal(idx, true_idx)
+    assert np.array_equal(rec.view(np.uint32), x.view(np.uint32))
+
+
+def test_error_follows_the_per_coordinate_recursion():
+    rng = np.random.default_rng(3)
+    pa, pb = ocb.twin_pools()
+    u = osr.projection_matrix() / 8.0                           # orthonormal basis of col(U)
+    for pools, sigmas, scale in ((pa, (0.06,) * 3, 0.06), (pb, (0.0025, 0.001, 0.0005), 0.0025)):
+        x = scale * rng.standard_normal((4096, 64))
+        _, rec, _ = osr.rvq_encode_blocks(x.astype(np.float32), pools)
+        err = x.astype(np.float32).astype(np.float64) - rec.astype(np.float64)
+        perp = x.astype(np.float32).astype(np.float64)
+        perp = perp - perp @ u @ u.T
+        assert np.allclose(err - err @ u @ u.T, perp, atol=1e-6)
+        e = x.astype(np.float32).astype(np.float64) @ u
+        for s in sigmas:
+            e = e - np.where(e > 0, 1.0, -1.0) * (8.0 * s / 3.0)
+        assert np.allclose(err @ u, e, atol=1e-6)
