@@ -6,13 +6,16 @@
 // k_l from the residual, adds pool[l][k_l] to the reconstruction and subtracts it from the
 // residual, in fp32 and in that order (lithe/quant.py:54-71).
 //
-// Layout: a block is handled by one 16-lane DPP row; lane j holds values 4j .. 4j + 3 (one 16-byte
-// load, so a wave's load instruction covers four whole blocks = 1 KB of whole lines). Per level each
-// lane forms the nine signed partial sums of its four values, and four DPP steps (swap within
-// pairs, swap pairs of a quad, half-row mirror, row mirror) reduce them over the row: every lane
-// ends with the same nine sums (fp32 addition is commutative, so both partners of a step compute
-// the same value). The codeword value at position t is the value-table lookup
-// lut[l][popcount((k ^ m_t) & 511)] of the bulk decode.
+// Layout: a block is handled by one 16-lane DPP row. Lane (quad c, position i) holds the four values
+// t = 16 i + 4 c + e, e < 4 (one 16-byte load; a wave's load instruction covers four whole blocks),
+// so quad c owns the residues t mod 16 = 4 c + e. Since q < 16, (-1)^popcount(t & q) factorises as
+// (-1)^popcount(e & (q & 3)) (-1)^popcount(c & (q >> 2)), and the nine projections are
+//   p_q = sum_c (-1)^popcount(c & (q >> 2)) H_c[q & 3],  H_c[g] = sum over the quad of W[g],
+// with W the 4-point Walsh transform of a lane's four values. Per level: W in the lane, H by two
+// DPP steps inside the quad (swap pairs, swap halves), then each p_q by two DPP steps across the
+// quads (half-row mirror, row mirror). Both partners of every step add the same two values, so all
+// sixteen lanes end with bit-identical projections and the same index. The codeword value at
+// position t is the value-table lookup lut[l][popcount((k ^ m_t) & 511)] of the bulk decode.
 #include <stdint.h>
 
 #include "lithe_common.h"
@@ -23,14 +26,14 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kBlocksPerWave = 4;              // 64 lanes / 16 lanes per block
 
-__device__ __forceinline__ float dpp_sum16(float v) {
-    // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-    return v;
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+constexpr int kQuadSwapPairs = 0xB1;    // quad_perm [1, 0, 3, 2]
+constexpr int kQuadSwapHalves = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kRowHalfMirror = 0x141;   // lane i <-> 7 - i within each half row
+constexpr int kRowMirror = 0x140;       // lane i <-> 15 - i
 
 template <typename IdxT>
 __global__ void __launch_bounds__(kThreads) encode_kernel(const float *__restrict__ blocks, int64_t n,
@@ -41,32 +44,34 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(const float *__restric
     if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&luts.v[0][0][0])[threadIdx.x];
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int lane = threadIdx.x & 63, j = lane & 15, c = j >> 2, i = j & 3;
     const int64_t blk = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * kBlocksPerWave + (lane >> 4);
     const bool valid = blk < n;
     const int64_t b = valid ? blk : n - 1;           // clamped: every lane of a row loads and reduces
-    f32x4 r = *reinterpret_cast<const f32x4 *>(blocks + b * kBlock + 4 * j);
+    const int t0 = 16 * i + 4 * c;
+    f32x4 r = *reinterpret_cast<const f32x4 *>(blocks + b * kBlock + t0);
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    // sign bits of this lane's four positions for the nine hyperplanes; codeword masks m_t
-    uint32_t neg[4], mt[4];
+    uint32_t mt[4];                                  // codeword masks of this lane's positions
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint32_t t = (uint32_t)(4 * j + e);
-        uint32_t s = 0;
-#pragma unroll
-        for (int q = 0; q < 9; ++q) s |= (uint32_t)(__builtin_popcount(t & (uint32_t)q) & 1) << q;
-        neg[e] = s;
-        mt[e] = sign_mask(t & 15u);
-    }
+    for (int e = 0; e < 4; ++e) mt[e] = sign_mask((uint32_t)(4 * c + e));
+    const bool neg1 = c & 1, neg2 = c & 2;           // quad signs of q >> 2 = 1 and 2
     for (int l = 0; l < levels; ++l) {
+        // 4-point Walsh transform of the lane's values, then the sum over the quad
+        const float a0 = r[0] + r[1], a1 = r[0] - r[1], a2 = r[2] + r[3], a3 = r[2] - r[3];
+        float h[4] = {a0 + a2, a1 + a3, a0 - a2, a1 - a3};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            h[g] += dpp<kQuadSwapPairs>(h[g]);
+            h[g] += dpp<kQuadSwapHalves>(h[g]);
+        }
         uint32_t k = 0;
 #pragma unroll
         for (int q = 0; q < 9; ++q) {
-            float p = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p += ((neg[e] >> q) & 1u) ? -r[e] : r[e];
-            p = dpp_sum16(p);
+            const float hv = h[q & 3];
+            float p = (q >> 2) == 0 ? hv : (q >> 2) == 1 ? (neg1 ? -hv : hv) : (neg2 ? -hv : hv);
+            p += dpp<kRowHalfMirror>(p);
+            p += dpp<kRowMirror>(p);
             k |= (p > 0.0f ? 1u : 0u) << q;
         }
         const float *tab = lut + (sides && sides[b] ? kMaxLevels * 10 : 0) + l * 10;
@@ -78,7 +83,7 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(const float *__restric
         }
         if (valid && j == 0) idx[(int64_t)l * level_stride + blk * block_stride] = (IdxT)k;
     }
-    if (recon && valid) *reinterpret_cast<f32x4 *>(recon + blk * kBlock + 4 * j) = acc;
+    if (recon && valid) *reinterpret_cast<f32x4 *>(recon + blk * kBlock + t0) = acc;
 }
 
 }  // namespace
