@@ -6,16 +6,19 @@
 // k_l from the residual, adds pool[l][k_l] to the reconstruction and subtracts it from the
 // residual, in fp32 and in that order (lithe/quant.py:54-71).
 //
-// Layout: a block is handled by one 16-lane DPP row. Lane (quad c, position i) holds the four values
-// t = 16 i + 4 c + e, e < 4 (one 16-byte load; a wave's load instruction covers four whole blocks),
-// so quad c owns the residues t mod 16 = 4 c + e. Since q < 16, (-1)^popcount(t & q) factorises as
-// (-1)^popcount(e & (q & 3)) (-1)^popcount(c & (q >> 2)), and the nine projections are
-//   p_q = sum_c (-1)^popcount(c & (q >> 2)) H_c[q & 3],  H_c[g] = sum over the quad of W[g],
-// with W the 4-point Walsh transform of a lane's four values. Per level: W in the lane, H by two
-// DPP steps inside the quad (swap pairs, swap halves), then each p_q by two DPP steps across the
-// quads (half-row mirror, row mirror). Both partners of every step add the same two values, so all
-// sixteen lanes end with bit-identical projections and the same index. The codeword value at
-// position t is the value-table lookup lut[l][popcount((k ^ m_t) & 511)] of the bulk decode.
+// Layout: a block is handled by one quad. Lane c of the quad holds the sixteen values
+// t = 16 i + 4 c + e (i, e < 4; four 16-byte loads at 64-byte steps), so it owns the residues
+// t mod 16 = 4 c + e. Because q < 16, the projection on column q depends on t mod 16 only, and
+// with q = 4 h + g, (-1)^popcount(t & q) = (-1)^popcount(c & h) (-1)^popcount(e & g):
+//   fold      s[e] = sum_i r[16 i + 4 c + e]                       (in the lane)
+//   Walsh     w_c[g] = sum_e (-1)^popcount(e & g) s[e]             (in the lane)
+//   butterfly p[4 h + g] = sum_c (-1)^popcount(c & h) w_c[g]       (two DPP steps over the quad)
+// after which lane h holds p[4 h .. 4 h + 3]; each lane sets the index bits of its own
+// projections and two DPP ORs give every lane of the quad the whole index. The codeword of
+// level l is periodic in t with period 16, so the residual stays folded: s[e] -= 4 c_l[4 c + e]
+// (exact: the fold of a 16-periodic block is 4 times its period). The reconstruction is the
+// level-order fp32 sum of the codewords, written as four copies of the lane's four values.
+// The codeword value at position t is lut[l][popcount((k ^ m_t) & 511)], as in the bulk decode.
 #include <stdint.h>
 
 #include "lithe_common.h"
@@ -24,16 +27,22 @@ namespace lithe {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBlocksPerWave = 4;              // 64 lanes / 16 lanes per block
+constexpr int kBlocksPerWave = 16;             // 64 lanes / 4 lanes per block
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-constexpr int kQuadSwapPairs = 0xB1;    // quad_perm [1, 0, 3, 2]
-constexpr int kQuadSwapHalves = 0x4E;   // quad_perm [2, 3, 0, 1]
-constexpr int kRowHalfMirror = 0x141;   // lane i <-> 7 - i within each half row
-constexpr int kRowMirror = 0x140;       // lane i <-> 15 - i
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kQuadSwapPairs = 0xB1;    // quad_perm [1, 0, 3, 2]: lane c <-> c ^ 1
+constexpr int kQuadSwapHalves = 0x4E;   // quad_perm [2, 3, 0, 1]: lane c <-> c ^ 2
+
+__device__ __forceinline__ float flip_sign(float v, uint32_t sign) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) ^ sign);
+}
 
 template <typename IdxT>
 __global__ void __launch_bounds__(kThreads) encode_kernel(const float *__restrict__ blocks, int64_t n,
@@ -44,46 +53,54 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(const float *__restric
     if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&luts.v[0][0][0])[threadIdx.x];
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, j = lane & 15, c = j >> 2, i = j & 3;
-    const int64_t blk = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * kBlocksPerWave + (lane >> 4);
+    const int lane = threadIdx.x & 63, c = lane & 3;
+    const int64_t blk = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * kBlocksPerWave + (lane >> 2);
     const bool valid = blk < n;
-    const int64_t b = valid ? blk : n - 1;           // clamped: every lane of a row loads and reduces
-    const int t0 = 16 * i + 4 * c;
-    f32x4 r = *reinterpret_cast<const f32x4 *>(blocks + b * kBlock + t0);
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    uint32_t mt[4];                                  // codeword masks of this lane's positions
+    const int64_t b = valid ? blk : n - 1;           // clamped: every lane of a quad loads and exchanges
+    const float *src = blocks + b * kBlock + 4 * c;
+    f32x4 r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) mt[e] = sign_mask((uint32_t)(4 * c + e));
-    const bool neg1 = c & 1, neg2 = c & 2;           // quad signs of q >> 2 = 1 and 2
+    for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const f32x4 *>(src + 16 * i);
+    float s[4], acc[4];
+    uint32_t mt[4];                                  // codeword masks of this lane's residues
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        s[e] = (r[0][e] + r[1][e]) + (r[2][e] + r[3][e]);
+        acc[e] = 0.0f;
+        mt[e] = sign_mask((uint32_t)(4 * c + e)) & kIndexMask;
+    }
+    const uint32_t sign1 = (c & 1) ? 0x80000000u : 0u, sign2 = (c & 2) ? 0x80000000u : 0u;
+    const float *tab = lut + (sides && sides[b] ? kMaxLevels * 10 : 0);
+    uint32_t own = 0;                                // the index of level c, stored by lane c
     for (int l = 0; l < levels; ++l) {
-        // 4-point Walsh transform of the lane's values, then the sum over the quad
-        const float a0 = r[0] + r[1], a1 = r[0] - r[1], a2 = r[2] + r[3], a3 = r[2] - r[3];
-        float h[4] = {a0 + a2, a1 + a3, a0 - a2, a1 - a3};
+        const float a0 = s[0] + s[1], a1 = s[0] - s[1], a2 = s[2] + s[3], a3 = s[2] - s[3];
+        const float w[4] = {a0 + a2, a1 + a3, a0 - a2, a1 - a3};
+        uint32_t bits = 0;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            h[g] += dpp<kQuadSwapPairs>(h[g]);
-            h[g] += dpp<kQuadSwapHalves>(h[g]);
+            float p = dpp<kQuadSwapPairs>(w[g]) + flip_sign(w[g], sign1);
+            p = dpp<kQuadSwapHalves>(p) + flip_sign(p, sign2);
+            bits |= (p > 0.0f ? 1u : 0u) << g;
         }
-        uint32_t k = 0;
-#pragma unroll
-        for (int q = 0; q < 9; ++q) {
-            const float hv = h[q & 3];
-            float p = (q >> 2) == 0 ? hv : (q >> 2) == 1 ? (neg1 ? -hv : hv) : (neg2 ? -hv : hv);
-            p += dpp<kRowHalfMirror>(p);
-            p += dpp<kRowMirror>(p);
-            k |= (p > 0.0f ? 1u : 0u) << q;
-        }
-        const float *tab = lut + (sides && sides[b] ? kMaxLevels * 10 : 0) + l * 10;
+        uint32_t k = (bits << (4 * c)) & kIndexMask;
+        k |= dpp<kQuadSwapPairs>(k);
+        k |= dpp<kQuadSwapHalves>(k);
+        own = c == l ? k : own;
+        const float *tl = tab + l * 10;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float c = tab[__builtin_popcount((k ^ mt[e]) & kIndexMask)];
-            acc[e] += c;
-            r[e] -= c;
+            const float v = tl[__builtin_popcount(k ^ mt[e])];
+            acc[e] += v;
+            s[e] = fmaf(-4.0f, v, s[e]);
         }
-        if (valid && j == 0) idx[(int64_t)l * level_stride + blk * block_stride] = (IdxT)k;
     }
-    if (recon && valid) *reinterpret_cast<f32x4 *>(recon + blk * kBlock + t0) = acc;
+    if (valid && c < levels) idx[(int64_t)c * level_stride + blk * block_stride] = (IdxT)own;
+    if (recon && valid) {
+        float *dst = recon + blk * kBlock + 4 * c;
+        const f32x4 v = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4 *>(dst + 16 * i) = v;
+    }
 }
 
 }  // namespace

@@ -167,7 +167,9 @@ __device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
 // the stream. A fragments come from LDS (ds_read) while x streams through the vector
 // memory path. Waves that split a token group's K range reduce their fp32 partials
 // through LDS in a fixed order (deterministic).
-template <typename XT, int SRC, int GM, int U>
+// XNT: x loads carry the non-temporal hint (x is read once). The replicated shared-input form
+// reads each x line from several workgroups of one XCD and keeps it in L2 instead.
+template <typename XT, int SRC, int GM, int U, bool XNT>
 __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     constexpr bool kBf16 = sizeof(XT) == 2;
@@ -391,7 +393,7 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
 #pragma unroll
         for (int j = 0; j < U; ++j) {
             const int st = 2 * (j >> 1) + (lc >> 2);    // step of this lane's chunk inside the batch
-            bt.x[j] = stream_load<XV, true>(
+            bt.x[j] = stream_load<XV, XNT>(
                 reinterpret_cast<const XV *>(st < d.n ? lrow[j & 1] + (int64_t)KSTEP * (d.s0 + st) : dummy));
         }
     };
@@ -1017,9 +1019,21 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     return p;
 }
 
+#ifndef LITHE_SHARED_X_NT
+#define LITHE_SHARED_X_NT 0
+#endif
+
 template <typename XT, int SRC, int GM>
 void launch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU>),
+    if constexpr (SRC != SRC_DENSE && !LITHE_SHARED_X_NT) {
+        if (a.n_mod_wg > 1) {    // replicated shared-input shrink: x stays in L2 for the other modules
+            hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU, false>),
+                               dim3((unsigned)((a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg)), dim3(kThreads),
+                               p.lds_s, st, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU, true>),
                        dim3((unsigned)(a.n_mod_wg > 1 ? (a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg
                                                       : a.n_batch * p.tiles_s)),
                        dim3(kThreads), p.lds_s, st, a);

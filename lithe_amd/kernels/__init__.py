@@ -17,7 +17,7 @@ their restatement is the test oracle under ``oracle/``.
 from ._hip import HAS_HIP, gpu_available, workspace_errors
 from .bank import PackedBank
 from .layers import IndexLoRALinear, PerSampleLoRALinear, wrap_linears
-from .packed import (PackedLayout, decode_int16, decode_packed, decode_packed_slots, decode_packed_stacked,
+from .packed import (PackedLayout, blockify_factors, decode_int16, decode_packed, decode_packed_slots, decode_packed_stacked,
                      flat_indices, pack_adapter, pack_indices, split_decoded, split_stacked, unpack_indices)
 from .sgmv import per_sample_lora_delta
 from .shared import packed_lora_delta, shared_codebook_lora_delta
@@ -25,7 +25,7 @@ from .shared import packed_lora_delta, shared_codebook_lora_delta
 __all__ = [
     "HAS_HIP", "gpu_available", "workspace_errors",
     "IndexLoRALinear", "PerSampleLoRALinear", "wrap_linears", "PackedBank",
-    "PackedLayout", "decode_packed", "decode_packed_slots", "decode_packed_stacked", "decode_int16",
+    "PackedLayout", "blockify_factors", "decode_packed", "decode_packed_slots", "decode_packed_stacked", "decode_int16",
     "flat_indices", "pack_adapter", "pack_indices", "split_decoded", "split_stacked", "unpack_indices",
     "per_sample_lora_delta", "packed_lora_delta", "shared_codebook_lora_delta",
 ]

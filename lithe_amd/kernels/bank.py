@@ -16,7 +16,7 @@ import torch
 
 from .. import codebook as cb
 from . import _hip
-from .packed import (PackedLayout, decode_packed_slots, decode_packed_stacked, pack_adapter, split_decoded,
+from .packed import (PackedLayout, blockify_factors, decode_packed_slots, decode_packed_stacked, pack_adapter, split_decoded,
                      split_stacked)
 
 
@@ -239,16 +239,7 @@ class PackedBank:
         ``lithe/kernels/packed.py:136-143``). Returns the slot id."""
         lay = self.layout
         bs = lay.block_size
-        blocks = torch.zeros((lay.total_blocks, bs), dtype=torch.float32, device=self.device)
-        for name, sa, sb, ao, bo in zip(lay.names, lay.shapes_a, lay.shapes_b, lay.a_off, lay.b_off):
-            if name not in factors:
-                raise ValueError(f"missing factors of module {name}")
-            a, b = factors[name]
-            if tuple(a.shape) != sa or tuple(b.shape) != sb:
-                raise ValueError(f"{name}: factors {tuple(a.shape)} / {tuple(b.shape)}, layout {sa} / {sb}")
-            for w, off in ((a, ao), (b, bo)):
-                flat = w.detach().reshape(-1).to(device=self.device, dtype=torch.float32)
-                blocks.view(-1)[off * bs: off * bs + flat.numel()].copy_(flat)
+        blocks = blockify_factors(lay, factors, self.device)
         L = lay.num_levels
         idx = torch.empty(lay.total_blocks * L, dtype=torch.int16, device=self.device)
         lut_a = _hip.lut_from_pools(self.pool_a, torch.float32)

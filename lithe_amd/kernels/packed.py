@@ -191,6 +191,41 @@ def flat_indices(ad, layout: PackedLayout) -> np.ndarray:
     return np.concatenate(parts).astype(np.uint16) if parts else np.zeros(0, np.uint16)
 
 
+def blockify_factors(layout: PackedLayout, factors: Dict[str, Tuple[torch.Tensor, torch.Tensor]],
+                     device) -> torch.Tensor:
+    """Dense factors {module: (A (r, d_in), B (d_out, r))} -> (total_blocks, block_size) fp32 on
+    ``device``: each factor row-major blockified at its layout offset, zero-padded to whole blocks
+    (``lithe/quant.py:23-43`` per factor, in residency order). One concatenation builds it; zero
+    runs appear only where a factor does not fill its last block."""
+    bs = layout.block_size
+    segs = []
+    for name, sa, sb, ao, bo in zip(layout.names, layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
+        if name not in factors:
+            raise ValueError(f"missing factors of module {name}")
+        a, b = factors[name]
+        if tuple(a.shape) != sa or tuple(b.shape) != sb:
+            raise ValueError(f"{name}: factors {tuple(a.shape)} / {tuple(b.shape)}, layout {sa} / {sb}")
+        segs.append((ao * bs, a))
+        segs.append((bo * bs, b))
+    segs.sort(key=lambda s: s[0])
+    total = layout.total_blocks * bs
+    bounds = [(off, off + w.numel()) for off, w in segs] + [(total, total)]
+    if any(nxt < end for (_, end), (nxt, _) in zip(bounds, bounds[1:])):
+        raise ValueError("layout offsets overlap")
+    gaps = [nxt - end for (_, end), (nxt, _) in zip([(0, 0)] + bounds, bounds)]
+    zeros = torch.zeros(max(gaps), dtype=torch.float32, device=device)
+    parts = []
+    for (_, w), gap in zip(segs + [(None, None)], gaps):
+        if gap:
+            parts.append(zeros[:gap])
+        if w is not None:
+            parts.append(w.detach().reshape(-1).to(device=device, dtype=torch.float32))
+    out = torch.empty((layout.total_blocks, bs), dtype=torch.float32, device=device)
+    if parts:
+        torch.cat(parts, out=out.view(-1))
+    return out
+
+
 def pack_adapter(ad, layout: Optional[PackedLayout] = None) -> Tuple[torch.Tensor, PackedLayout]:
     """(packed uint64 words on CPU, layout) for one ``LitheAdapter``."""
     if ad.n_bits != INDEX_BITS:

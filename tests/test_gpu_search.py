@@ -90,7 +90,7 @@ def test_bank_encode_factors_matches_oracle():
     greedy encode of its factor (pool A for A, pool B for B) wherever the margin is clear."""
     from lithe_amd.kernels import PackedBank, PackedLayout
     from oracle import packing as opk
-    mods = [("q", 256, 384), ("odd", 96, 40), ("up", 128, 512)]
+    mods = [("q", 256, 384), ("odd", 96, 40), ("pad", 90, 41), ("up", 128, 512)]
     lay = PackedLayout.from_modules([{"name": n, "shape_a": [16, di], "shape_b": [do, 16]} for n, di, do in mods])
     bank = PackedBank(lay, "cuda", capacity=2)
     g = torch.Generator().manual_seed(11)

@@ -3,6 +3,7 @@ brute force over all 512 codewords, exact round trips of lattice points, and the
 per-coordinate error recursion of the nine orthogonal Hadamard directions
 (tests/test_quant.py:17-74 of the reference, restated)."""
 import numpy as np
+import pytest
 
 from oracle import codebook as ocb
 from oracle import decode as odec
@@ -52,3 +53,25 @@ def test_error_follows_the_per_coordinate_recursion():
         for s in sigmas:
             e = e - np.where(e > 0, 1.0, -1.0) * (8.0 * s / 3.0)
         assert np.allclose(err @ u, e, atol=1e-6)
+
+
+def test_blockify_factors_places_every_factor_at_its_offset():
+    """The encoder's input: every factor row-major blockified (zero-padded) at its layout offset,
+    A blocks before B blocks per module, as the oracle's per-factor blockify lays them out."""
+    import torch
+
+    from lithe_amd.kernels import PackedLayout, blockify_factors
+    from oracle import packing as opk
+    mods = [("q", 16, 256, 384), ("pad", 16, 90, 41), ("odd", 5, 7, 3), ("up", 16, 128, 512)]
+    lay = PackedLayout.from_modules([{"name": n, "shape_a": [r, di], "shape_b": [do, r]} for n, r, di, do in mods])
+    g = torch.Generator().manual_seed(5)
+    factors = {n: (torch.randn(r, di, generator=g), torch.randn(do, r, generator=g).bfloat16())
+               for n, r, di, do in mods}
+    got = blockify_factors(lay, factors, "cpu").numpy()
+    want = np.concatenate([opk.blockify(f.float().numpy()) for n, *_ in mods for f in factors[n]])
+    assert got.shape == want.shape == (lay.total_blocks, 64)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    with pytest.raises(ValueError, match="missing factors"):
+        blockify_factors(lay, {k: v for k, v in factors.items() if k != "pad"}, "cpu")
+    with pytest.raises(ValueError, match="layout"):
+        blockify_factors(lay, {**factors, "odd": (factors["odd"][1], factors["odd"][0])}, "cpu")
