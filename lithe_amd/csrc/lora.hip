@@ -56,6 +56,10 @@ constexpr int kHead = 256;
 static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
 constexpr int kFillBatch = 3;     // fill items per thread whose loads are issued together
 constexpr int kShrinkU = 4;       // k-steps per shrink load batch (even: loads move step pairs)
+#ifndef LITHE_EXCHANGE_OUTPUTS
+#define LITHE_EXCHANGE_OUTPUTS 128
+#endif
+constexpr int kExchangeOutputs = LITHE_EXCHANGE_OUTPUTS;   // outputs per expand LDS exchange (whole-line y)
 
 // Factor sources: SRC_PACKED is SRC_INDEXED with both index streams PACKED9 with 3 levels (the
 // resident bank of the twin codebook), compiled without the kind dispatch of the other index
@@ -615,6 +619,33 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
 
     constexpr int NP = BOM / 32;
     const int np = a.BO / 32;
+
+    // Whole-line y path (bf16 y): rows of this wave's two 8-token halves of sub-tile `sub`, and
+    // its y loads (access j: token 8 (j & 1) + lane / 8, outputs 64 (j >> 1) + 8 (lane % 8) ..).
+    // They are issued per sub-tile, after the B tile is built: vector loads complete in order,
+    // so y loads issued ahead of the B index loads would hold up the decode behind them
+    // (measured: 1.8 % slower sweep).
+    constexpr int NJ = BOM / 32;
+    const int64_t omax = a.d_out - 8;
+    auto line_rows = [&](int sub, int64_t *lrow, bool *lval) __attribute__((always_inline)) {
+#pragma unroll
+        for (int eta = 0; eta < 2; ++eta) {
+            const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + 8 * eta + (lane >> 3);
+            lval[eta] = m < a.seq;
+            lrow[eta] = (b * a.seq + (lval[eta] ? m : a.seq - 1)) * a.d_out;
+        }
+    };
+    auto line_load = [&](int sub, bf16x8 *yv) __attribute__((always_inline)) {
+        int64_t lrow[2];
+        bool lval[2];
+        line_rows(sub, lrow, lval);
+        const __bf16 *yb = static_cast<const __bf16 *>(a.y);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            yv[j] = stream_load<bf16x8, true>(reinterpret_cast<const bf16x8 *>(
+                yb + lrow[j & 1] + std::min<int64_t>(obase + 64 * (j >> 1) + 8 * (lane & 7), omax)));
+    };
+
     // mid fragments; groups without an adapter read group 0 of the same row (their B
     // fragments are zero), so every lane issues the same unconditional loads.
     int gsrc[GM];
@@ -796,19 +827,21 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
 
     // ---- sub-tiles: 16 tokens per wave each. Every load of a sub-tile is issued up front
     // (rows and columns clamped in range); waves of other workgroups hide the latency.
-    const int64_t omax = a.d_out - 8;
 
     // Whole-line y path (bf16 y). The y tile of a wave (16 tokens x BOM outputs) moves in
     // loads and stores that each cover whole 128-byte lines: access j gives lane L token
     // 8 (j & 1) + L / 8 and outputs 64 (j >> 1) + 8 (L % 8) .. + 7, with the non-temporal hint
     // (measured: +5 % read-modify-write bandwidth; split-line accesses lose with it). The
     // delta d = round_y(round_y(acc) * s) is finished in the MFMA layout (lane: token r16,
-    // outputs 32 p + 8 gq ..) and exchanged through a per-wave LDS tile: 16-byte unit
-    // (token t, chunk q) at (BOM / 8) t + (q ^ swz(t)), conflict-free for both sides at BOM >= 128.
-    constexpr int NJ = BOM / 32;
-    auto line_subtile = [&](int sub, const Frag *mf) __attribute__((always_inline)) {
-        __bf16 *stg = reinterpret_cast<__bf16 *>(smem + a.estage_off) + wave * 16 * BOM;
-        constexpr int RU = BOM / 8;    // 16-byte units per token row of the tile
+    // outputs 32 p + 8 gq ..) and exchanged through a per-wave LDS tile, HB outputs at a time
+    // (a 4 KB tile: the workgroup's LDS stays small enough for 8 workgroups per CU): 16-byte
+    // unit (token t, chunk q) at (HB / 8) t + (q ^ swz(t)), conflict-free for both sides at
+    // HB >= 128. A wave reuses its tile for the next half after reading it back (LDS accesses
+    // of one wave complete in order).
+    constexpr int HB = kExchangeOutputs < BOM ? kExchangeOutputs : BOM;   // outputs per exchange
+    auto line_subtile = [&](int sub, const Frag *mf, const bf16x8 *yv) __attribute__((always_inline)) {
+        __bf16 *stg = reinterpret_cast<__bf16 *>(smem + a.estage_off) + wave * 16 * HB;
+        constexpr int RU = HB / 8;     // 16-byte units per token row of the tile
         auto unit = [&](int t, int q) __attribute__((always_inline)) {
             const int swz = ((t & 7) | ((((t >> 3) ^ t) & 1) << 3)) & (RU - 1);
             return stg + (RU * t + (q ^ swz)) * 8;
@@ -816,44 +849,36 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
         const int lr = lane >> 3, lc = lane & 7;
         int64_t lrow[2];
         bool lval[2];
-#pragma unroll
-        for (int eta = 0; eta < 2; ++eta) {
-            const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + 8 * eta + lr;
-            lval[eta] = m < a.seq;
-            lrow[eta] = (b * a.seq + (lval[eta] ? m : a.seq - 1)) * a.d_out;
-        }
+        line_rows(sub, lrow, lval);
         __bf16 *yb = static_cast<__bf16 *>(a.y);
-        bf16x8 yv[NJ];
-        if constexpr (ACC) {
+        constexpr int PH = HB / 32;    // MFMA column groups (and y accesses) per exchange
 #pragma unroll
-            for (int j = 0; j < NJ; ++j)
-                yv[j] = stream_load<bf16x8, true>(reinterpret_cast<const bf16x8 *>(
-                    yb + lrow[j & 1] + std::min<int64_t>(obase + 64 * (j >> 1) + 8 * lc, omax)));
-        }
+        for (int h = 0; h < BOM / HB; ++h) {
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            if (p >= np) break;
-            float vals[8];
-            compute(mf, p, vals);
-            bf16x8 d;
+            for (int p = h * PH; p < (h + 1) * PH; ++p) {
+                if (p >= np) break;
+                float vals[8];
+                compute(mf, p, vals);
+                bf16x8 d;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) d[e] = (__bf16)(DT<YT>::round(vals[e]) * s_b);
-            *reinterpret_cast<bf16x8 *>(unit(r16, 4 * p + gq)) = d;
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int t = 8 * (j & 1) + lr, q = 8 * (j >> 1) + lc;
-            const bf16x8 d = *reinterpret_cast<const bf16x8 *>(unit(t, q));
-            const int64_t o8 = obase + 8 * q;
-            bf16x8 out;
-            if constexpr (ACC) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) out[e] = (__bf16)((float)yv[j][e] + (float)d[e]);
-            } else {
-                out = d;
+                for (int e = 0; e < 8; ++e) d[e] = (__bf16)(DT<YT>::round(vals[e]) * s_b);
+                *reinterpret_cast<bf16x8 *>(unit(r16, 4 * (p - h * PH) + gq)) = d;
             }
-            if (lval[j & 1] && 8 * q < a.BO && o8 < a.d_out)
-                stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + lrow[j & 1] + o8), out);
+#pragma unroll
+            for (int j = h * PH; j < (h + 1) * PH; ++j) {
+                const int t = 8 * (j & 1) + lr, q = 8 * (j >> 1) + lc;
+                const bf16x8 d = *reinterpret_cast<const bf16x8 *>(unit(t, q - h * RU));
+                const int64_t o8 = obase + 8 * q;
+                bf16x8 out;
+                if constexpr (ACC) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) out[e] = (__bf16)((float)yv[j][e] + (float)d[e]);
+                } else {
+                    out = d;
+                }
+                if (lval[j & 1] && 8 * q < a.BO && o8 < a.d_out)
+                    stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + lrow[j & 1] + o8), out);
+            }
         }
     };
     for (int sub = 0; sub < a.subs_e; ++sub) {
@@ -871,7 +896,9 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
         YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
         if constexpr (LINE) {
             if (a.vec_y) {
-                line_subtile(sub, mf);
+                bf16x8 yv[NJ];
+                if (ACC) line_load(sub, yv);
+                line_subtile(sub, mf, yv);
                 continue;
             }
         }
@@ -1011,7 +1038,8 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.lds_e = kHead + (dense ? (size_t)n_route * p.BO * rank * xbytes : (size_t)n_route * p.nblk_max * 16 * xbytes);
     // whole-line y path (bf16 y, output tiles of whole lines): a 16 x BOM bf16 tile per wave
     p.estage_off = (int)((p.lds_e + 15) & ~size_t(15));
-    if (ybytes == 2 && p.BOM % 64 == 0) p.lds_e = p.estage_off + (size_t)kWaves * 16 * p.BOM * 2;
+    if (ybytes == 2 && p.BOM % 64 == 0)
+        p.lds_e = p.estage_off + (size_t)kWaves * 16 * std::min(p.BOM, kExchangeOutputs) * 2;
 
     // workspace: [error word | mid]
     p.off_mid = 256;
