@@ -1,11 +1,14 @@
-"""Blocking and the residual decode of the twin Hadamard codebook.
+"""Blocking, the residual decode and the greedy residual encode of the twin Hadamard codebook.
 
-API of ``lithe/quant.py:23-43, 74-92`` (the decode half). A factor of any shape
-is flattened row-major, zero-padded to a multiple of the 64-value block and
-viewed as (n_blocks, 64). ``rvq_decode_blocks`` runs on the GPU through
-``lithe_decode``: the L levels are summed in fp32 in level order, the same
-order as the reference, so the result is bit-identical. The encode half
-(search, STE) belongs to training and is not part of this library.
+API of ``lithe/quant.py:23-92``. A factor of any shape is flattened row-major,
+zero-padded to a multiple of the 64-value block and viewed as (n_blocks, 64).
+``rvq_decode_blocks`` runs on the GPU through ``lithe_decode``: the L levels are
+summed in fp32 in level order, the same order as the reference, so the result is
+bit-identical. ``nearest_index`` / ``rvq_encode_blocks`` / ``encode`` run on the
+GPU through ``lithe_encode`` (the closed-form search: bit q of a level's index is
+set exactly when the residual's projection on Hadamard column q is positive). The
+straight-through estimator (``ste``) belongs to training and is not part of this
+library.
 """
 from __future__ import annotations
 
@@ -38,6 +41,37 @@ def num_blocks(shape, block_size: int = cb.BLOCK_SIZE) -> int:
     for s in shape:
         n *= int(s)
     return -(-n // block_size)
+
+
+_UNIT_POOL = {}     # device -> (1, 512, 64) unit-scale pool (a level's scale does not move the argmin)
+
+
+def nearest_index(x: torch.Tensor, proj: torch.Tensor) -> torch.Tensor:
+    """Index (N,) int64 of the nearest codeword of every 64-value block of ``x`` (N, 64)
+    (``lithe/quant.py:46-51``); ``proj`` must be the codebook's Hadamard generator. Every
+    codeword of a level has one norm, so the index does not depend on the level's scale."""
+    from .kernels import search
+    search._check_proj(proj, x.shape[-1])
+    key = str(x.device)
+    if key not in _UNIT_POOL:
+        _UNIT_POOL[key] = cb.build_pools([1.0], x.shape[-1]).to(x.device)
+    idx, _ = search._encode(x, _UNIT_POOL[key], want_recon=False)
+    return idx[0]
+
+
+def rvq_encode_blocks(blocks: torch.Tensor, pools: torch.Tensor,
+                      proj: torch.Tensor) -> "tuple[torch.Tensor, torch.Tensor]":
+    """Greedy residual encode: (indices (L, N) int64, reconstruction (N, 64) fp32)
+    (``lithe/quant.py:54-71``), all levels in one launch."""
+    from .kernels import search
+    return search.rvq_encode_blocks_fast(blocks, pools, proj)
+
+
+def encode(w: torch.Tensor, pools: torch.Tensor, proj: torch.Tensor) -> "tuple[torch.Tensor, torch.Tensor]":
+    """Quantise a factor of any shape: (indices (L, n_blocks) int64, w_hat with w's shape)
+    (``lithe/quant.py:84-88``)."""
+    from .kernels import search
+    return search.encode(w, pools, proj)
 
 
 def rvq_decode_blocks(indices: torch.Tensor, pools: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
