@@ -161,3 +161,53 @@ def test_decode_bad_slot_zero_fills_and_flags():
             assert np.array_equal(got, bits), i
         else:
             assert not got.any(), i      # bf16 +0.0 everywhere
+
+
+def test_decode_side_table_unaligned_and_tail():
+    """Layouts of more than 2**21 blocks read a workgroup's 1,024 side bytes with 4-byte loads
+    where they can; a side table at an odd address and the partial last workgroup take the byte
+    path. Both forms give the oracle's bits: a small layout (2,058 blocks, byte path throughout)
+    at an aligned and an odd address here; the rank-64 FLUX layout in the next test."""
+    from lithe_amd.kernels import _delta
+    from lithe_amd.kernels.packed import _decode
+    ad = random_adapter([("m0", 1024, 1024), ("m1", 1024, 2048), ("m2", 512, 2600)], rank=16, seed=4)
+    _, bits, _ = _oracle_decode_bits(ad)
+    words, layout = pack_adapter(ad)
+    n = layout.total_blocks
+    assert n % 1024 != 0 and n > 2048
+    pa, pb = (p.cuda() for p in lithe_amd.twin_pools())
+    w = words.cuda()
+    aligned = decode_packed(w, layout, pa, pb)
+    assert np.array_equal(aligned.view(torch.int16).cpu().numpy().view(np.uint16), bits)
+    buf = torch.zeros(n + 1, dtype=torch.int8, device="cuda")
+    buf[1:].copy_(layout.sides.cuda())
+    odd = buf[1:]
+    assert odd.data_ptr() % 4 != 0
+    s = _delta.packed_source(w.view(1, -1), layout.num_levels, 0)
+    out = torch.empty((n, 64), dtype=torch.bfloat16, device="cuda")
+    _decode(s, n, odd, pa, pb, out)
+    assert torch.equal(out, aligned)
+
+
+def test_decode_rank64_flux_layout_staged_sides():
+    """The rank-64 FLUX layout plus one small module (2,801,768 blocks: side bytes through LDS,
+    and a partial last workgroup) against the C restatement, aligned and at an odd side-table
+    address."""
+    from lithe_amd.kernels import _delta
+    from lithe_amd.kernels.packed import _decode
+    ad = random_adapter(flux_modules() + [("extra", 64, 40)], rank=64, seed=12)
+    words, layout = pack_adapter(ad)
+    n = layout.total_blocks
+    assert n == 2_801_768 and n > 2 ** 21 and n % 1024 != 0
+    pa, pb = ocb.twin_pools()
+    ref_bits = native.decode(words.view(torch.int64).numpy().view(np.uint64), n, 3,
+                             layout.sides.numpy(), pa, pb, want="bf16")
+    pa_t, pb_t = (p.cuda() for p in lithe_amd.twin_pools())
+    w = words.cuda()
+    out = decode_packed(w, layout, pa_t, pb_t)
+    assert np.array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), ref_bits)
+    buf = torch.zeros(n + 1, dtype=torch.int8, device="cuda")
+    buf[1:].copy_(layout.sides.cuda())
+    out2 = torch.empty_like(out)
+    _decode(_delta.packed_source(w.view(1, -1), layout.num_levels, 0), n, buf[1:], pa_t, pb_t, out2)
+    assert torch.equal(out2, out)
