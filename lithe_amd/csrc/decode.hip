@@ -157,25 +157,28 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 // index loads of all of them before decoding the first, so a wave keeps ITER round trips in
 // flight instead of one; the workgroup count drops ITER-fold. Output order and values are
 // those of decode_kernel.
-// Side bytes. A side table that stays in L2 (at most kStageSidesBlocks bytes, half of one XCD's
-// L2) is read with one byte load per half-block, issued after the index loads. A larger one is
-// evicted by the output stream between uses, and a workgroup (kSpan consecutive blocks from
-// blockIdx.x * kSpan) then reads its sides with one coalesced 4-byte load per thread, issued
-// after the index loads, and takes them from LDS (measured: rank 64, 2.8 MB of sides, +6 %;
-// rank 16, 0.7 MB, -3 %). In both forms every wave finishes its loads before its first store
-// (stores that start while a workgroup's index loads are landing cost 6 % at rank 16). The last
-// workgroup of a selection, or a side table not 4-byte aligned, reads the bytes one by one.
-constexpr int kDecodeIter = 8;
-constexpr int kSpan = kThreads * kDecodeIter / 2;
+// Side bytes and layout size. A side table that stays in L2 (at most kStageSidesBlocks bytes,
+// half of one XCD's L2) is read with one byte load per half-block, issued after the index loads,
+// with 8 half-blocks per thread. A larger one is evicted by the output stream between uses: a
+// workgroup (SPAN consecutive blocks from blockIdx.x * SPAN) then reads its sides with coalesced
+// 4-byte loads issued after the index loads and takes them from LDS, and each thread owns 16
+// half-blocks (measured at rank 64, 2.8 MB of sides: 3.95 -> 4.19 TB/s from the staging, -> 4.47
+// with 16 half-blocks; at rank 16, 0.7 MB, the staged form is 3 % slower and 16 half-blocks gain
+// 0.3 %). In both forms every wave finishes its loads before its first store (stores that start
+// while a workgroup's index loads are landing cost 6 % at rank 16). The last workgroup of a
+// selection, or a side table not 4-byte aligned, reads the bytes one by one.
 constexpr int64_t kStageSidesBlocks = int64_t(1) << 21;
-static_assert(kSpan == 4 * kThreads, "one 4-byte side load per thread");
+constexpr int decode_iter(bool stage) { return stage ? 16 : 8; }
 template <typename OutT, bool STAGE>
 __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) {
+    constexpr int kDecodeIter = decode_iter(STAGE);
+    constexpr int SPAN = kThreads * kDecodeIter / 2;
+    static_assert(SPAN % (4 * kThreads) == 0, "whole 4-byte side loads per thread");
     __shared__ float lut[2 * kMaxLevels * 10];
-    __shared__ int8_t wg_side[STAGE ? kSpan : 4];
+    __shared__ int8_t wg_side[STAGE ? SPAN : 4];
     if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
-    const int64_t b0 = (int64_t)blockIdx.x * kSpan;
-    const bool whole = STAGE && a.sides && b0 + kSpan <= a.n_blocks &&
+    const int64_t b0 = (int64_t)blockIdx.x * SPAN;
+    const bool whole = STAGE && a.sides && b0 + SPAN <= a.n_blocks &&
                        (reinterpret_cast<uintptr_t>(a.sides) & 3u) == 0;
 
     const int sel = blockIdx.y;
@@ -197,8 +200,13 @@ __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) 
     }
     load_raw<kDecodeIter, true, 3>(a.src, sl, blk, raw);
     if (STAGE && whole) {
-        const uint32_t sw = *reinterpret_cast<const uint32_t *>(a.sides + b0 + 4 * (int64_t)threadIdx.x);
-        *reinterpret_cast<uint32_t *>(wg_side + 4 * threadIdx.x) = sw;
+        uint32_t sw[SPAN / (4 * kThreads)];
+#pragma unroll
+        for (int q = 0; q < SPAN / (4 * kThreads); ++q)
+            sw[q] = *reinterpret_cast<const uint32_t *>(a.sides + b0 + 4 * (int64_t)(threadIdx.x + q * kThreads));
+#pragma unroll
+        for (int q = 0; q < SPAN / (4 * kThreads); ++q)
+            *reinterpret_cast<uint32_t *>(wg_side + 4 * (threadIdx.x + q * kThreads)) = sw[q];
     } else {
 #pragma unroll
         for (int i = 0; i < kDecodeIter; ++i) side[i] = a.sides ? a.sides[blk[i]] : 0;
@@ -361,8 +369,9 @@ static int32_t decode_impl(const lithe_index_src *src, const int32_t *slots, int
     a.n_sel = n_sel;
     const int64_t halves = n_blocks * 2;
     if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3) {
-        dim3 grid((unsigned)((halves + kThreads * kDecodeIter - 1) / (kThreads * kDecodeIter)), (unsigned)n_sel);
         const bool stage = n_blocks > kStageSidesBlocks;
+        const int64_t per_wg = (int64_t)kThreads * decode_iter(stage);
+        dim3 grid((unsigned)((halves + per_wg - 1) / per_wg), (unsigned)n_sel);
         if (out_dtype == LITHE_DT_BF16) {
             if (stage) hipLaunchKernelGGL((decode_packed3_kernel<__bf16, true>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);
             else hipLaunchKernelGGL((decode_packed3_kernel<__bf16, false>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);

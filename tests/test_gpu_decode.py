@@ -164,7 +164,7 @@ def test_decode_bad_slot_zero_fills_and_flags():
 
 
 def test_decode_side_table_unaligned_and_tail():
-    """Layouts of more than 2**21 blocks read a workgroup's 1,024 side bytes with 4-byte loads
+    """Layouts of more than 2**21 blocks read a workgroup's side bytes with 4-byte loads
     where they can; a side table at an odd address and the partial last workgroup take the byte
     path. Both forms give the oracle's bits: a small layout (2,058 blocks, byte path throughout)
     at an aligned and an odd address here; the rank-64 FLUX layout in the next test."""
