@@ -194,3 +194,79 @@ def test_product_entry_points_refuse_cpu_tensors():
         decode_packed(words, layout, pa, pb)
     with pytest.raises(RuntimeError):
         unpack_indices(words.view(torch.int64), 7)
+
+
+def test_shared_x_argument_errors_before_any_launch():
+    """lithe_lora_delta_shared_x: host arrays, one shared A source, group-count limit."""
+    lib = _hip.load()
+    f0, words = _indexed()
+    slot = np.zeros(2, dtype=np.int32)
+    route = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=None, slot_scale=None, n_route=1)
+
+    def call(fs, n_mod=None, d_outs=None, ys=None, scales=None, n_batch=2, wsb=1 << 20, rte=route):
+        n = len(fs) if n_mod is None else n_mod
+        fa = (_hip.Factors * max(1, len(fs)))(*fs) if fs else None
+        ya = (ctypes.c_void_p * max(1, n))(*(ys or [1 << 12] * n))
+        da = (ctypes.c_int64 * max(1, n))(*(d_outs or [64] * n))
+        sa = (ctypes.c_float * max(1, n))(*(scales or [1.0] * n))
+        return lib.lithe_lora_delta_shared_x(ctypes.c_void_p(1 << 12), _hip.DT_BF16, n_batch, 8, 128, n, ya,
+                                             _hip.DT_BF16, da, 1, 16, fa, ctypes.byref(rte) if rte else None,
+                                             None, sa, ctypes.c_void_p(1 << 12), wsb, None)
+
+    fq, fk, fv = _indexed()[0], _indexed()[0], _indexed()[0]
+    for f in (fq, fk, fv):
+        f.a_idx.base = f0.a_idx.base
+        f.b_idx.base = f0.b_idx.base
+    assert call([]) == _hip.ERR_NULL                                          # no factors
+    assert call([fq, fk, fv], rte=None) == _hip.ERR_NULL
+    assert call([fq, fk, fv], n_mod=0) == _hip.ERR_SHAPE
+    assert call([fq] * 9) == _hip.ERR_SHAPE                                   # 9 rank groups > 8
+    assert call([fq, fk, fv], d_outs=[64, 0, 64]) == _hip.ERR_SHAPE
+    assert call([fq, fk, fv], ys=[1 << 12, 0, 1 << 12]) == _hip.ERR_NULL
+    assert call([fq, fk, fv], ys=[1 << 12, (1 << 12) + 1, 1 << 12]) == _hip.ERR_ALIGN
+    other = _indexed()[0]                                                     # A in another bank
+    other.a_idx.base = f0.a_idx.base + 4096
+    assert call([fq, other, fv]) == _hip.ERR_UNSUPPORTED
+    lut2 = _indexed()[0]
+    lut2.a_idx.base, lut2.b_idx.base = f0.a_idx.base, f0.b_idx.base
+    lut2.lut_a.value[0][3] = 0.5                                              # another A value table
+    assert call([fq, lut2, fv]) == _hip.ERR_UNSUPPORTED
+    dense = _hip.Factors()
+    dense.kind = _hip.FACTOR_DENSE
+    assert call([fq, dense, fv]) == _hip.ERR_UNSUPPORTED
+    assert call([fq, fk, fv], wsb=256) == _hip.ERR_WORKSPACE
+    assert call([fq, fk, fv], n_batch=0) == _hip.OK                           # empty batch: nothing to do
+    del words
+
+
+def test_encode_decode_stacked_ingest_argument_errors():
+    lib = _hip.load()
+    lut = _hip.Lut(num_levels=3)
+    P = ctypes.c_void_p(1 << 12)
+    enc = lib.lithe_encode
+    assert enc(P, -1, None, ctypes.byref(lut), None, P, _hip.DT_I16, 5, 1, None, None) == _hip.ERR_SHAPE
+    assert enc(P, 5, None, None, None, P, _hip.DT_I16, 5, 1, None, None) == _hip.ERR_NULL
+    assert enc(P, 5, P, ctypes.byref(lut), None, P, _hip.DT_I16, 5, 1, None, None) == _hip.ERR_NULL  # sides, no lut_b
+    bad = _hip.Lut(num_levels=5)
+    assert enc(P, 5, None, ctypes.byref(bad), None, P, _hip.DT_I16, 5, 1, None, None) == _hip.ERR_LEVELS
+    assert enc(P, 5, None, ctypes.byref(lut), None, P, _hip.DT_BF16, 5, 1, None, None) == _hip.ERR_DTYPE
+    assert enc(P, 0, None, ctypes.byref(lut), None, None, _hip.DT_I16, 0, 1, None, None) == _hip.OK
+    assert enc(None, 5, None, ctypes.byref(lut), None, P, _hip.DT_I16, 5, 1, None, None) == _hip.ERR_NULL
+    assert enc(P, 5, None, ctypes.byref(lut), None, P, _hip.DT_I16, 2, 1, None, None) == _hip.ERR_SHAPE  # overlap
+    assert enc(P, 5, None, ctypes.byref(lut), None, P, _hip.DT_I16, 1, 2, None, None) == _hip.ERR_SHAPE
+    assert enc(ctypes.c_void_p((1 << 12) + 4), 5, None, ctypes.byref(lut), None, P, _hip.DT_I16, 5, 1, None,
+               None) == _hip.ERR_ALIGN
+    src = _hip.IndexSrc(base=1 << 12, kind=_hip.IDX_PACKED9, num_levels=3, slot_stride=10, level_stride=0,
+                        block_off=0, n_slots=1)
+    ds = lib.lithe_decode_stacked
+    assert ds(ctypes.byref(src), None, 1, 4, 2, None, None, ctypes.byref(lut), ctypes.byref(lut), P, _hip.DT_BF16,
+              None, None) == _hip.ERR_NULL                                    # no segment table
+    assert ds(ctypes.byref(src), None, 1, 4, 0, P, None, ctypes.byref(lut), ctypes.byref(lut), P, _hip.DT_BF16,
+              None, None) == _hip.ERR_SHAPE
+    ing = lib.lithe_ingest
+    assert ing(P, -1, 3, 2, P, P, 10, None, None) == _hip.ERR_SHAPE
+    assert ing(P, 7, 3, 0, P, P, 10, None, None) == _hip.ERR_SHAPE
+    assert ing(P, 7, 0, 2, P, P, 10, None, None) == _hip.ERR_LEVELS
+    assert ing(P, 70, 3, 2, P, P, 9, None, None) == _hip.ERR_SHAPE             # 70 indices need 10 words
+    assert ing(None, 0, 3, 2, None, None, 0, None, None) == _hip.OK
+    assert ing(None, 7, 3, 2, P, P, 1, None, None) == _hip.ERR_NULL
