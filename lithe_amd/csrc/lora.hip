@@ -55,7 +55,15 @@ constexpr int kLutFloats = kMaxLevels * 10;
 constexpr int kHead = 256;
 static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
 constexpr int kFillBatch = 3;     // fill items per thread whose loads are issued together
-constexpr int kShrinkU = 4;       // k-steps per shrink load batch (even: loads move step pairs)
+#ifndef LITHE_SHRINK_U
+#define LITHE_SHRINK_U 4
+#endif
+#ifndef LITHE_STAGE_LOADS
+#define LITHE_STAGE_LOADS 2    // one step pair at a time: a 2 KB stage per wave (measured 0.2 % faster than 4 KB)
+#endif
+constexpr int kShrinkU = LITHE_SHRINK_U;         // k-steps per shrink load batch (even: loads move step pairs)
+constexpr int kStageLoads = LITHE_STAGE_LOADS;   // loads of a batch that pass through the LDS stage at once
+static_assert(kShrinkU % kStageLoads == 0 && kStageLoads % 2 == 0, "the stage takes whole step pairs");
 #ifndef LITHE_EXCHANGE_OUTPUTS
 #define LITHE_EXCHANGE_OUTPUTS 128
 #endif
@@ -376,9 +384,11 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     // (chunk c = step 2 pi + c / 4, bytes 16 (c % 4) of it). Whole-line loads take the
     // non-temporal hint (measured: +15 % read bandwidth; split-line loads lose with it).
     // The MFMA wants lane (token r16, group gq) to hold chunk 4 sigma + gq of step 2 pi + sigma,
-    // so every batch goes through a per-wave LDS staging area: 16-byte unit (pi, t, c) at
-    // pi * 128 + 8 t + (c ^ (t >> 1)) (the XOR keeps both the writes and the reads free of
-    // bank conflicts).
+    // so every batch goes through a per-wave LDS staging area, one step pair (two loads, 2 KB)
+    // at a time by default: 16-byte unit (pi, t, c) at pi * 128 + 8 t + (c ^ (t >> 1)), pi
+    // counted inside the staged part (the XOR keeps both the writes and the reads free of bank
+    // conflicts). A wave reuses its stage for the next pair after reading it (LDS accesses of
+    // one wave complete in order).
     static_assert(U % 2 == 0, "x loads move pairs of k-steps");
     const int lr = lane >> 3, lc = lane & 7;
     const XT *lrow[2];
@@ -389,7 +399,8 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
                     (lc & 3) * EV;
     }
     const XT *dummy = static_cast<const XT *>(a.x);
-    char *stage = smem + a.stage_off + wave * (U * 1024);
+    constexpr int SL = kStageLoads < U ? kStageLoads : U;   // loads staged at a time
+    char *stage = smem + a.stage_off + wave * (SL * 1024);
     struct Batch {
         XV x[U];
     };
@@ -401,53 +412,63 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
                 reinterpret_cast<const XV *>(st < d.n ? lrow[j & 1] + (int64_t)KSTEP * (d.s0 + st) : dummy));
         }
     };
-    auto stage_batch = [&](const Batch &bt) __attribute__((always_inline)) {
+    // loads [m SL, (m + 1) SL) of a batch (steps of the same range) pass through the stage together
+    auto stage_batch = [&](const Batch &bt, int m) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < U; ++j) {
+        for (int j = m * SL; j < (m + 1) * SL; ++j) {
             const int t = 8 * (j & 1) + lr;
-            *reinterpret_cast<XV *>(stage + ((j >> 1) * 128 + 8 * t + (lc ^ (t >> 1))) * 16) = bt.x[j];
+            *reinterpret_cast<XV *>(stage + (((j - m * SL) >> 1) * 128 + 8 * t + (lc ^ (t >> 1))) * 16) = bt.x[j];
         }
     };
-    auto staged = [&](int u) __attribute__((always_inline)) -> XV {
+    auto staged = [&](int u, int m) __attribute__((always_inline)) -> XV {
         const int c = 4 * (u & 1) + gq;
-        return *reinterpret_cast<const XV *>(stage + ((u >> 1) * 128 + 8 * r16 + (c ^ (r16 >> 1))) * 16);
+        return *reinterpret_cast<const XV *>(stage + (((u - m * SL) >> 1) * 128 + 8 * r16 + (c ^ (r16 >> 1))) * 16);
     };
     f32x4 acc[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto compute_batch = [&](const Batch &bt, const Desc &d) __attribute__((always_inline)) {
-        stage_batch(bt);
-        XV xv[U];
+    auto compute_chunk = [&](const Batch &bt, const Desc &d, const XT *reg, int sp, int m) __attribute__((always_inline)) {
+        stage_batch(bt, m);
+        XV xv[SL];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (u < d.n) xv[u] = staged(u);
-        const XT *reg = ring + (d.g & 1) * a.region + r16 * a.arow;
-        const int sp = d.s0 - d.g * pb * SPB;    // step inside the piece
-        XV av[U][GM];
+        for (int v = 0; v < SL; ++v)
+            if (m * SL + v < d.n) xv[v] = staged(m * SL + v, m);
+        XV av[SL][GM];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int v = 0; v < SL; ++v)
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
+                const int u = m * SL + v;
                 const XT *ap;
                 if constexpr (SRC != SRC_DENSE)
                     ap = reg + g * 16 * a.arow + (kBf16 ? ((sp + u) >> 1) * 16 + 8 * (gq & 1) : ((sp + u) >> 2) * 16 + 4 * gq);
                 else
                     ap = reg + g * 16 * a.arow + (sp + u) * KSTEP + (kBf16 ? 8 : 4) * gq;
-                if (u < d.n) av[u][g] = *reinterpret_cast<const XV *>(ap);
+                if (u < d.n) av[v][g] = *reinterpret_cast<const XV *>(ap);
             }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (u >= d.n) break;
+        for (int v = 0; v < SL; ++v) {
+            if (m * SL + v >= d.n) break;
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
                 if constexpr (kBf16) {
-                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][g], xv[u], acc[g], 0, 0, 0);
+                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[v][g], xv[v], acc[g], 0, 0, 0);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][g][e], xv[u][e], acc[g], 0, 0, 0);
+                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[v][g][e], xv[v][e], acc[g], 0, 0, 0);
                 }
             }
+        }
+    };
+
+    auto compute_batch = [&](const Batch &bt, const Desc &d) __attribute__((always_inline)) {
+        const XT *reg = ring + (d.g & 1) * a.region + r16 * a.arow;
+        const int sp = d.s0 - d.g * pb * SPB;    // step inside the piece
+#pragma unroll
+        for (int m = 0; m < U / SL; ++m) {
+            if (m * SL >= d.n) break;
+            compute_chunk(bt, d, reg, sp, m);
         }
     };
 
@@ -1017,7 +1038,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     const int64_t npiece = (d_in / kBlock + p.pb - 1) / p.pb;
     p.red_off = kHead + (npiece > 1 ? 2 : 1) * p.region * xbytes;
     p.stage_off = p.red_off + (ks > 1 ? kWaves * p.GM * 64 * 16 : 0);
-    p.lds_s = p.stage_off + (size_t)kWaves * kShrinkU * 1024;
+    p.lds_s = p.stage_off + (size_t)kWaves * std::min(kStageLoads, kShrinkU) * 1024;
 
     // expand: BO outputs x 64*subs tokens per workgroup.
     int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
