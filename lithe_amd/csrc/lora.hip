@@ -643,9 +643,10 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
 
     // Whole-line y path (bf16 y): rows of this wave's two 8-token halves of sub-tile `sub`, and
     // its y loads (access j: token 8 (j & 1) + lane / 8, outputs 64 (j >> 1) + 8 (lane % 8) ..).
-    // They are issued per sub-tile, after the B tile is built: vector loads complete in order,
-    // so y loads issued ahead of the B index loads would hold up the decode behind them
-    // (measured: 1.8 % slower sweep).
+    // They are issued per sub-tile, after the B tile is built. Issued earlier they cost the
+    // sweep 1.8 % ahead of the B index loads (the decode waits behind them: loads complete in
+    // order) and 2.6 % right behind them (the decode does not wait, but the tile's y registers
+    // stay live through the decode and the barrier).
     constexpr int NJ = BOM / 32;
     const int64_t omax = a.d_out - 8;
     auto line_rows = [&](int sub, int64_t *lrow, bool *lval) __attribute__((always_inline)) {
