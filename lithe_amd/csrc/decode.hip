@@ -312,6 +312,7 @@ extern "C" int32_t lithe_unpack9(const uint64_t *words, int64_t n, void *out, in
     if (!words || !out) return LITHE_ERR_NULL;
     const int64_t n_words = (n + 6) / 7;
     const int64_t grid = (n_words + kThreads - 1) / kThreads;
+    if (grid > kMaxGridX) return LITHE_ERR_SHAPE;
     hipLaunchKernelGGL(unpack9_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, words, n,
                        out, out_dtype);
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
@@ -327,6 +328,7 @@ extern "C" int32_t lithe_pack9(const void *idx, int32_t idx_dtype, int64_t n, ui
     if (!idx || !words) return LITHE_ERR_NULL;
     const int64_t n_words = (n + 6) / 7;
     const int64_t grid = (n_words + kThreads - 1) / kThreads;
+    if (grid > kMaxGridX) return LITHE_ERR_SHAPE;
     hipLaunchKernelGGL(pack9_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, idx, idx_dtype,
                        n, words, err_flag);
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
@@ -368,6 +370,8 @@ static int32_t decode_impl(const lithe_index_src *src, const int32_t *slots, int
     a.n_seg = n_seg;
     a.n_sel = n_sel;
     const int64_t halves = n_blocks * 2;
+    // the widest grid is the one-half-block-per-thread kernel's
+    if ((halves + kThreads - 1) / kThreads > kMaxGridX || n_sel > kMaxGridY) return LITHE_ERR_SHAPE;
     if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3) {
         const bool stage = n_blocks > kStageSidesBlocks;
         const int64_t per_wg = (int64_t)kThreads * decode_iter(stage);

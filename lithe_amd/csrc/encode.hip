@@ -130,6 +130,7 @@ extern "C" int32_t lithe_encode(const float *blocks, int64_t n, const int8_t *si
             for (int p = 0; p < 10; ++p) luts.v[s][l][p] = t->value[l][p];
     }
     const int64_t per_wg = (kThreads / 64) * kBlocksPerWave;
+    if ((n + per_wg - 1) / per_wg > kMaxGridX) return LITHE_ERR_SHAPE;
     const dim3 grid((unsigned)((n + per_wg - 1) / per_wg));
     hipStream_t st = (hipStream_t)stream;
     if (idx_dtype == LITHE_DT_I16)

@@ -71,6 +71,7 @@ extern "C" int32_t lithe_ingest(const uint16_t *stream, int64_t n_stream, int32_
     if (n_words == 0) return LITHE_OK;
     if (!stream || !table || !words) return LITHE_ERR_NULL;
     const int64_t grid = (n_words + kThreads - 1) / kThreads;
+    if (grid > kMaxGridX) return LITHE_ERR_SHAPE;
     hipLaunchKernelGGL(ingest_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)hip_stream, stream,
                        n_stream, num_levels, n_segments, table, words, n_words, err_flag);
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;

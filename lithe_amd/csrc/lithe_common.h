@@ -23,6 +23,10 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBlock = 64;
+// Launch limits: workgroups along x (and along y, where a launch uses it); larger problems are
+// rejected with LITHE_ERR_SHAPE before any launch.
+constexpr int64_t kMaxGridX = 0x7fffffff;
+constexpr int64_t kMaxGridY = 65535;
 constexpr int kMaxLevels = 4;
 constexpr uint32_t kIndexMask = 0x1FFu;
 

@@ -1234,6 +1234,14 @@ int32_t check_indexed(const lithe_factors *f, int32_t rank, int64_t d_in, int64_
     return LITHE_OK;
 }
 
+// Workgroup counts of the shrink (n_mod_wg > 1: replicated shared-input layout, padded to whole
+// XCD rounds) and of the expand (bounded over its sub-tile choices) fit a launch.
+bool grids_fit(const Plan &p, int64_t n_batch, int64_t d_out, int n_mod_wg) {
+    const int64_t shrink = n_mod_wg > 1 ? (n_batch * p.tiles_s + 7) / 8 * 8 * n_mod_wg : n_batch * p.tiles_s;
+    const int64_t expand = ((d_out + p.BO - 1) / p.BO) * n_batch * p.tiles_e * p.subs_e;
+    return shrink <= kMaxGridX && expand <= kMaxGridX;
+}
+
 void copy_lut(float dst[kMaxLevels][10], const lithe_lut &l) {
     for (int v = 0; v < kMaxLevels; ++v)
         for (int q = 0; q < 10; ++q) dst[v][q] = l.value[v][q];
@@ -1313,6 +1321,7 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
 
     const Plan p = make_plan(n_batch, seq, d_in, d_out, rank, routes->n_route, xbytes, f->kind == LITHE_FACTOR_DENSE,
                              ybytes);
+    if (!grids_fit(p, n_batch, d_out, 1)) return LITHE_ERR_SHAPE;
     if (workspace_bytes < p.total) return LITHE_ERR_WORKSPACE;
     set_call_fields(a, x, static_cast<char *>(workspace), p, n_batch, seq, d_in, rank, routes, mid_scale);
     set_module_fields(a, y, d_out, accumulate, out_scale, out_scale_vec);
@@ -1360,6 +1369,7 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
         d_out_max = std::max(d_out_max, d_out[m]);
     }
     const Plan ps = make_plan(n_batch, seq, d_in, d_out_max, rank, routes->n_route * n_mod, xbytes, false, ybytes);
+    if (!grids_fit(ps, n_batch, d_out_max, n_mod)) return LITHE_ERR_SHAPE;
     if (workspace_bytes < ps.total) return LITHE_ERR_WORKSPACE;
 
     LoraArgs a{};

@@ -270,3 +270,23 @@ def test_encode_decode_stacked_ingest_argument_errors():
     assert ing(P, 70, 3, 2, P, P, 9, None, None) == _hip.ERR_SHAPE             # 70 indices need 10 words
     assert ing(None, 0, 3, 2, None, None, 0, None, None) == _hip.OK
     assert ing(None, 7, 3, 2, P, P, 1, None, None) == _hip.ERR_NULL
+
+
+def test_launch_grid_limits():
+    """Problems whose workgroup count would not fit a launch are rejected before any launch."""
+    lib = _hip.load()
+    f, words = _indexed(d_in=128, d_out=64)
+    slot = np.zeros(65535, dtype=np.int32)
+    route = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=None, slot_scale=None, n_route=1)
+    # 65,535 samples of 2**30 tokens: far more than 2**31 - 1 workgroups
+    assert _delta(lib, f, route, n_batch=65535, seq=1 << 30, wsb=1 << 62) == _hip.ERR_SHAPE
+    lut = _hip.Lut(num_levels=3)
+    P = ctypes.c_void_p(1 << 12)
+    assert lib.lithe_encode(P, 1 << 40, None, ctypes.byref(lut), None, P, _hip.DT_I16, 1 << 41, 1, None,
+                            None) == _hip.ERR_SHAPE
+    src = _hip.IndexSrc(base=1 << 12, kind=_hip.IDX_PACKED9, num_levels=3, slot_stride=10, level_stride=0,
+                        block_off=0, n_slots=1)
+    assert lib.lithe_decode(ctypes.byref(src), P, 70000, 4, None, ctypes.byref(lut), ctypes.byref(lut), P,
+                            _hip.DT_BF16, 256, None, None) == _hip.ERR_SHAPE       # 70,000 selections > 65,535
+    assert lib.lithe_unpack9(P, 1 << 45, P, _hip.DT_I64, None) == _hip.ERR_SHAPE
+    del words
