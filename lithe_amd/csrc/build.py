@@ -19,7 +19,9 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJ_DIR = os.path.join(HERE, "_obj")
 LIB_PATH = os.path.join(PKG, "_lib", "liblithe_amd.so")
 
-SOURCES = ["decode.hip", "lora.hip", "ingest.hip", "encode.hip", "host.cpp"]
+SOURCES = ["decode.hip", "lora.hip", "lora_shrink_bf16.hip", "lora_shrink_f32.hip", "lora_expand_bf16_bf16.hip",
+           "lora_expand_bf16_f32.hip", "lora_expand_f32_bf16.hip", "lora_expand_f32_f32.hip", "ingest.hip",
+           "encode.hip", "host.cpp"]
 ARCH = os.environ.get("LITHE_OFFLOAD_ARCH", "gfx950")
 
 

@@ -1,976 +1,10 @@
-// Per-sample LoRA delta with the factors decoded on the fly from index streams (or read dense):
-//
-//   shrink:  mid[row, g*16 + r] = round_x( sum_k x[row, k] * A_g[r, k] * mid_scale[b] )
-//   expand:  y[row, o]          = round_y( y + round_y( round_y( sum_{g,r} mid * B_g[o, r] ) * s_b ) )
-//
-// with A_g / B_g decoded in-kernel: value = round_x( w * sum_l lut[l][popc((k_l ^ m_t) & 511)] )
-// (B: ((d * slot_scale) * w), the reference's fold of alpha / r into B followed by the sqrt
-// mixture weight, lithe/serve.py:69-73, 89-96).
-//
-// The codewords repeat with period 16 (lithe_common.h), so a decoded 64-value block is
-// fully described by 16 values. Each shrink workgroup decodes the periods of its sample's
-// A rows for one K chunk straight from the index stream into LDS (a few KB of index words,
-// cache-resident after the first workgroup of the sample touches them); each expand
-// workgroup decodes the B periods of its output range the same way. Both issue the index
-// loads of a fill together and ahead of the tile's first activation loads (route slots and
-// weights come through scalar loads), so the decode waits for one memory round trip per K
-// chunk while the activation stream is already in flight, and needs no extra launch.
-//
-// g runs over "rank groups": route entry j of a sample contributes ceil(rank/16) groups of
-// 16 ranks (rank-stacked mixtures, lithe/serve.py:89-96).
-//
-// shrink  v_mfma_f32_16x16x32_bf16 (fp32: 16x16x4 f32), one wave per 16 tokens x K slice.
-//         A-operand = factor rows (lane%16 = rank), B-operand = x^T (lane%16 = token); lane
-//         group q = lane/16 owns k = 8q..8q+7 of each 32-wide step, so every row of x is read
-//         in 64-byte pieces. Loads are software-pipelined two batches deep with no branch
-//         between a load and its use. Waves that split one token group's K range reduce their
-//         fp32 partials through LDS in a fixed order (deterministic).
-// expand  v_mfma_f32_16x16x16_bf16 (fp32: 16x16x4 f32) with the factor B tile as the
-//         A-operand (lane%16 = output row) and mid^T as the B-operand (lane%16 = token).
-//         Output rows are assigned so that each lane ends with 8 consecutive outputs of its
-//         token: y is read-modified-written 16 bytes per lane with the reference's rounding
-//         chain applied in registers, the next sub-tile's loads in flight.
-#include <stdint.h>
-#include <stdlib.h>
-
-#include <algorithm>
-#include <type_traits>
-
-#include "lithe_common.h"
+// Host side of the per-sample LoRA delta: plans, argument checks and the C entry points
+// (lithe_lora_workspace_bytes, lithe_lora_delta, lithe_lora_delta_shared_x,
+// lithe_workspace_errors). The kernels are in lora_kernels.h.
+#include "lora_kernels.h"
 
 namespace lithe {
-
-bool src_covers(const lithe_index_src &s, int64_t n_blocks);
-int32_t validate_src(const lithe_index_src *s);
-IdxSrc make_src(const lithe_index_src &s);
-
 namespace {
-
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
-constexpr int kMaxGroups = 8;
-// Dynamic LDS head of both kernels: the value table of one side. The tile data (A chunk or
-// B periods) starts at kHead.
-constexpr int kLutFloats = kMaxLevels * 10;
-constexpr int kHead = 256;
-static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
-constexpr int kFillBatch = 3;     // fill items per thread whose loads are issued together
-#ifndef LITHE_SHRINK_U
-#define LITHE_SHRINK_U 4
-#endif
-#ifndef LITHE_STAGE_LOADS
-#define LITHE_STAGE_LOADS 2    // one step pair at a time: a 2 KB stage per wave (measured 0.2 % faster than 4 KB)
-#endif
-constexpr int kShrinkU = LITHE_SHRINK_U;         // k-steps per shrink load batch (even: loads move step pairs)
-constexpr int kStageLoads = LITHE_STAGE_LOADS;   // loads of a batch that pass through the LDS stage at once
-static_assert(kShrinkU % kStageLoads == 0 && kStageLoads % 2 == 0, "the stage takes whole step pairs");
-#ifndef LITHE_EXCHANGE_OUTPUTS
-#define LITHE_EXCHANGE_OUTPUTS 128
-#endif
-constexpr int kExchangeOutputs = LITHE_EXCHANGE_OUTPUTS;   // outputs per expand LDS exchange (whole-line y)
-
-// Factor sources: SRC_PACKED is SRC_INDEXED with both index streams PACKED9 with 3 levels (the
-// resident bank of the twin codebook), compiled without the kind dispatch of the other index
-// layouts and with the level count fixed.
-enum { SRC_INDEXED = 1, SRC_DENSE = 2, SRC_PACKED = 3 };
-constexpr int kPackedLevels = 3;
-template <int SRC> constexpr int fixed_levels() { return SRC == SRC_PACKED ? kPackedLevels : 0; }
-
-struct LoraArgs {
-    const void *x;
-    void *y;
-    void *mid;
-    int32_t *err;
-    int64_t n_batch, seq, d_in, d_out, rows;
-    int32_t rank, G, n_rg, n_route, MR;
-    int32_t tiles_s, ks, pb, arow, region, red_off, stage_off;
-    int32_t tiles_e, subs_e, BO, vec_y, nblk_max, estage_off;
-    int32_t accumulate;
-    float out_scale;
-    const int32_t *r_slot;
-    const float *r_w;
-    const float *s_scale;
-    const float *mid_scale;
-    const float *out_scale_vec;
-    IdxSrc a_src, b_src;
-    // Shared-input calls: the shrink's G groups are (module, route entry, rank group), module
-    // m = g / G1; group g's A blocks start at a_goff[g] (a_src.block_off is 0 in the kernels).
-    // The expand of one module reads mid groups [mid_goff, mid_goff + G).
-    int64_t a_goff[kMaxGroups];
-    int32_t G1, mid_goff;
-    // Replicated shared-input shrink: n_mod_wg > 1 launches one workgroup per (token tile, module),
-    // the modules of a tile on consecutive workgroup ids, so x is fetched from HBM once and the
-    // other modules' reads hit the Infinity Cache. Module mod's groups start at a_goff[mod]
-    // and write mid groups [mod * G, (mod + 1) * G).
-    int32_t n_mod_wg;
-    Luts luts;
-    const void *dense_a, *dense_b;
-    int64_t n_slots;
-};
-
-// Slot of route entry j of sample b, or -1 (empty entry or out of range; the latter is recorded).
-__device__ __forceinline__ int64_t route_slot(const LoraArgs &a, int64_t b, int j, bool record) {
-    const int32_t s = a.r_slot[b * a.n_route + j];
-    if (s >= 0 && (int64_t)s < a.n_slots) return s;
-    if (record && s != -1) record_error(a.err, kErrSlot);
-    return -1;
-}
-
-// m_t of lithe_common.h for a run-time t < 16: bit q of m_t is 1 ^ parity(t & q), and
-// parity(t & q) is linear in the bits of t (bit i of t flips the q that have bit i set).
-__host__ __device__ constexpr uint32_t sign_mask_rt(uint32_t t) {
-    return 0x1FFu ^ (((t & 1u) ? 0xAAu : 0u) ^ ((t & 2u) ? 0xCCu : 0u) ^ ((t & 4u) ? 0xF0u : 0u) ^
-                     ((t & 8u) ? 0x100u : 0u));
-}
-static_assert(sign_mask_rt(0) == sign_mask(0) && sign_mask_rt(5) == sign_mask(5) &&
-                  sign_mask_rt(10) == sign_mask(10) && sign_mask_rt(15) == sign_mask(15),
-              "linear form of the sign masks");
-
-// Activations and outputs are touched once per call: their loads and stores carry the
-// non-temporal hint, which keeps the streams from displacing the index words, the value
-// tables and the rank-r intermediate in L2 and the Infinity Cache (measured on MI355X:
-// +13 % read and +8 % read-modify-write bandwidth against plain accesses).
-#ifndef LITHE_STREAM_NT
-#define LITHE_STREAM_NT 0
-#endif
-template <typename V, bool FORCE_NT = false>
-__device__ __forceinline__ V stream_load(const V *p) {
-    if constexpr (FORCE_NT || LITHE_STREAM_NT) return __builtin_nontemporal_load(p);
-    else return *p;
-}
-template <typename V, bool FORCE_NT = false>
-__device__ __forceinline__ void stream_store(V *p, const V &v) {
-    if constexpr (FORCE_NT || LITHE_STREAM_NT) __builtin_nontemporal_store(v, p);
-    else *p = v;
-}
-
-template <typename XT>
-__device__ __forceinline__ void store16(XT *dst, const float v[16]) {
-    if constexpr (sizeof(XT) == 2) {
-        bf16x8 p0, p1;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            p0[t] = (__bf16)v[t];
-            p1[t] = (__bf16)v[8 + t];
-        }
-        reinterpret_cast<bf16x8 *>(dst)[0] = p0;
-        reinterpret_cast<bf16x8 *>(dst)[1] = p1;
-    } else {
-#pragma unroll
-        for (int t = 0; t < 16; t += 4) *reinterpret_cast<f32x4 *>(dst + t) = f32x4{v[t], v[t + 1], v[t + 2], v[t + 3]};
-    }
-}
-
-// One side's value table into LDS. The table sits in the kernel arguments, so lane 0
-// writes it from scalar registers: no vector load, nothing for later loads to wait behind.
-__device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
-    if (tid == 0) {
-#pragma unroll
-        for (int i = 0; i < kLutFloats; ++i) lut[i] = v[i];
-    }
-}
-
-// ============================================================================ shrink
-// Workgroup = 4 waves of one sample; each wave owns 16 tokens and 1/ks of every K piece
-// (ks waves share a token group). K is cut into pieces of pb blocks, and the sample's A
-// rows of a piece are decoded (dense factors: copied) into one of two LDS regions. The
-// piece after next is decoded while the current one streams, so the decode's ALU work
-// runs in the shadow of the activation loads and only piece 0 (and 1) sit in front of
-// the stream. A fragments come from LDS (ds_read) while x streams through the vector
-// memory path. Waves that split a token group's K range reduce their fp32 partials
-// through LDS in a fixed order (deterministic).
-// XNT: x loads carry the non-temporal hint (x is read once). The replicated shared-input form
-// reads each x line from several workgroups of one XCD and keeps it in L2 instead.
-template <typename XT, int SRC, int GM, int U, bool XNT>
-__global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    constexpr bool kBf16 = sizeof(XT) == 2;
-    constexpr int KSTEP = kBf16 ? 32 : 16;
-    constexpr int SPB = kBlock / KSTEP;      // k-steps per 64-value block
-    constexpr int EV = 16 / sizeof(XT);      // elements per 16-byte vector
-    typedef typename std::conditional<kBf16, bf16x8, f32x4>::type XV;
-
-    const int tid = threadIdx.x;
-    // wave index as a scalar: loop bounds derived from it stay uniform (SGPR) branches
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
-    const int ks = a.ks, tgw = kWaves / a.ks;
-    const int tgi = wave % tgw, ksi = wave / tgw;
-    // Replicated mode: workgroups are dealt round-robin to the 8 XCDs, so id w runs on XCD w % 8.
-    // The modules of tile t sit at ids 8 (M (t / 8) + m) + t % 8: one XCD, consecutive in its
-    // queue, sharing that XCD's L2 for x.
-    int mod = 0, tile = (int)blockIdx.x;
-    if (a.n_mod_wg > 1) {
-        const int q = (int)(blockIdx.x >> 3);
-        mod = q % a.n_mod_wg;
-        tile = (q / a.n_mod_wg) * 8 + (int)(blockIdx.x & 7);
-        if (tile >= (int)a.n_batch * a.tiles_s) return;    // padding of the last XCD round (before any barrier)
-    }
-    const int64_t b = tile / a.tiles_s;
-    const int mt = tile % a.tiles_s;
-    const int64_t m = ((int64_t)mt * tgw + tgi) * 16 + r16;
-    const bool valid = m < a.seq;
-    const int64_t row = b * a.seq + (valid ? m : a.seq - 1);
-
-    float *lut = reinterpret_cast<float *>(smem);
-    XT *ring = reinterpret_cast<XT *>(smem + kHead);
-    float *red = reinterpret_cast<float *>(smem + a.red_off);
-
-    // Per-group slot and mixture weight. b and g are uniform, so these are scalar loads
-    // (their own counter): nothing below waits behind them.
-    int32_t gs[GM];
-    float gw[GM];
-    bool any = false;
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        const int j = ((g < a.G ? g : 0) % a.G1) / a.n_rg;
-        gs[g] = g < a.G ? (int32_t)route_slot(a, b, j, false) : -1;
-        gw[g] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
-        any = any || gs[g] >= 0;
-    }
-    if (tid < GM && tid < a.G) route_slot(a, b, (tid % a.G1) / a.n_rg, true);   // records bad slot ids
-    if (!any) return;    // no adapter on this sample: no mid row is read for it
-    auto group_slot = [&](int g) __attribute__((always_inline)) -> int32_t {    // gs[g] for a run-time g < GM
-        int32_t r = gs[0];
-#pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? gs[q] : r;
-        return r;
-    };
-    auto group_weight = [&](int g) __attribute__((always_inline)) -> float {
-        float r = gw[0];
-#pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? gw[q] : r;
-        return r;
-    };
-    auto group_rank0 = [&](int g) __attribute__((always_inline)) -> int {   // (g % n_rg) * 16
-        int r = 0;
-#pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? (q % a.n_rg) * 16 : r;
-        return r;
-    };
-    // module of this workgroup's A in replicated mode (uniform), a_goff[mod]
-    int64_t mod_aoff = a.a_goff[0];
-#pragma unroll
-    for (int q = 1; q < kMaxGroups; ++q) mod_aoff = mod == q ? a.a_goff[q] : mod_aoff;
-    auto group_aoff = [&](int g) __attribute__((always_inline)) -> int64_t {   // a_goff[g], branch-free
-        if (a.n_mod_wg > 1) return mod_aoff;
-        int64_t r = a.a_goff[0];
-#pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? a.a_goff[q] : r;
-        return r;
-    };
-    if constexpr (SRC != SRC_DENSE) stage_lut(lut, a.luts.v[0][0], tid);
-
-    const int nb = (int)(a.d_in / kBlock);
-    const int pb = a.pb;
-    const int npiece = (nb + pb - 1) / pb;
-    auto piece_blocks = [&](int g) __attribute__((always_inline)) { return std::min(pb, nb - g * pb); };
-
-    // ---- fills. Indexed: item = the 16-value period of (row gr, block c) of piece g, at
-    // most kFillBatch items per thread (the plan keeps GM * 16 * pb <= kFillBatch * kThreads);
-    // the index loads of a piece are issued one piece ahead of its decode.
-    // item it of a piece: row gr = it % (GM*16), block c = it / (GM*16) (block-major: a shift)
-    constexpr int kRowsLog2 = GM == 1 ? 4 : GM == 2 ? 5 : GM == 4 ? 6 : 7;
-    auto idx_item = [&](int g, int it, int &gr, int &c, bool &live) __attribute__((always_inline)) -> int64_t {
-        gr = it & (GM * 16 - 1);
-        c = it >> kRowsLog2;
-        const int grp = gr >> 4;
-        const int rr = group_rank0(grp) + (gr & 15);
-        live = group_slot(grp) >= 0 && rr < a.rank;
-        return live ? group_aoff(grp) + (int64_t)rr * nb + (int64_t)g * pb + c : 0;
-    };
-    auto idx_load = [&](int g, RawIdx *dst) __attribute__((always_inline)) {
-        if (g >= npiece) return;
-        const int items = GM * 16 * piece_blocks(g);
-        int64_t slot[kFillBatch], blk[kFillBatch];
-#pragma unroll
-        for (int q = 0; q < kFillBatch; ++q) {
-            int gr, c;
-            bool live;
-            blk[q] = idx_item(g, std::min(q * kThreads + tid, items - 1), gr, c, live);
-            slot[q] = live ? group_slot(gr >> 4) : 0;
-        }
-        load_raw<kFillBatch, SRC == SRC_PACKED, fixed_levels<SRC>()>(a.a_src, slot, blk, dst);
-    };
-    auto idx_store = [&](int g, const RawIdx *src) __attribute__((always_inline)) {
-        if (g >= npiece) return;
-        const int items = GM * 16 * piece_blocks(g);
-        XT *reg = ring + (g & 1) * a.region;
-#pragma unroll
-        for (int q = 0; q < kFillBatch; ++q) {
-            const int it = q * kThreads + tid;
-            if (it >= items) break;
-            int gr, c;
-            bool live;
-            const int64_t blk = idx_item(g, it, gr, c, live);
-            uint32_t k[kMaxLevels];
-            const bool ok = extract_indices<SRC == SRC_PACKED, fixed_levels<SRC>()>(a.a_src, blk, src[q], k);
-            if (live && !ok) record_error(a.err, kErrIndex);
-            const float w = group_weight(gr >> 4);
-            float v[16];
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                // unconditional lookups, then a select: no branch between the table reads
-                const float d = decode_value<fixed_levels<SRC>()>(lut, a.a_src.levels, k, sign_mask(t)) * w;
-                v[t] = live ? d : 0.0f;
-            }
-            store16<XT>(reg + gr * a.arow + c * 16, v);
-            __builtin_amdgcn_sched_barrier(0);    // one item's values live at a time
-        }
-    };
-    // Dense: 16-byte pieces of the factor rows, loaded and stored batch by batch.
-    auto dense_fill = [&](int g) __attribute__((always_inline)) {
-        if (g >= npiece) return;
-        const int per_row = piece_blocks(g) * (kBlock / EV);
-        const int items = GM * 16 * per_row;
-        XT *reg = ring + (g & 1) * a.region;
-        for (int base = 0; base < items; base += kFillBatch * kThreads) {
-            f32x4 v[kFillBatch];
-#pragma unroll
-            for (int q = 0; q < kFillBatch; ++q) {
-                const int it = std::min(base + q * kThreads + tid, items - 1);
-                const int gr = it / per_row, c = it - gr * per_row;
-                const int grp = gr >> 4, rr = (grp % a.n_rg) * 16 + (gr & 15);
-                const bool live = group_slot(grp) >= 0 && rr < a.rank;
-                const int64_t off =
-                    live ? ((int64_t)group_slot(grp) * a.rank + rr) * a.d_in + (int64_t)g * pb * kBlock + c * EV : 0;
-                v[q] = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_a) + off);
-            }
-#pragma unroll
-            for (int q = 0; q < kFillBatch; ++q) {
-                const int it = base + q * kThreads + tid;
-                if (it >= items) break;
-                const int gr = it / per_row, c = it - gr * per_row;
-                const int grp = gr >> 4, rr = (grp % a.n_rg) * 16 + (gr & 15);
-                const bool live = group_slot(grp) >= 0 && rr < a.rank;
-                *reinterpret_cast<f32x4 *>(reg + gr * a.arow + c * EV) = live ? v[q] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-        }
-    };
-
-    // ---- this wave's k-steps: piece g contributes [g*pb*SPB + lo, g*pb*SPB + hi), cut into
-    // batches of at most U steps that never straddle two pieces.
-    struct Cur {
-        int g, s, hi;
-    };
-    struct Desc {
-        int g, s0, n;
-    };
-    auto share = [&](Cur &c) __attribute__((always_inline)) {
-        const int n = piece_blocks(c.g) * SPB;
-        c.s = c.g * pb * SPB + ksi * n / ks;
-        c.hi = c.g * pb * SPB + (ksi + 1) * n / ks;
-    };
-    auto skip_empty = [&](Cur &c) __attribute__((always_inline)) {
-        while (c.g < npiece && c.s >= c.hi) {
-            ++c.g;
-            if (c.g < npiece) share(c);
-        }
-    };
-    auto next = [&](Cur &c) __attribute__((always_inline)) -> Desc {
-        Desc d{npiece, 0, 0};
-        if (c.g >= npiece) return d;
-        d.g = c.g;
-        d.s0 = c.s;
-        d.n = std::min(U, c.hi - c.s);
-        c.s += d.n;
-        skip_empty(c);
-        return d;
-    };
-
-    // ---- x stream. A k-step is 64 bytes of a token row (32 bf16 or 16 fp32), so a pair of
-    // steps is one 128-byte line. Each load instruction covers whole lines: load (pair pi,
-    // half eta) gives lane L token 8 eta + L / 8 and 16-byte chunk c = L % 8 of the pair
-    // (chunk c = step 2 pi + c / 4, bytes 16 (c % 4) of it). Whole-line loads take the
-    // non-temporal hint (measured: +15 % read bandwidth; split-line loads lose with it).
-    // The MFMA wants lane (token r16, group gq) to hold chunk 4 sigma + gq of step 2 pi + sigma,
-    // so every batch goes through a per-wave LDS staging area, one step pair (two loads, 2 KB)
-    // at a time by default: 16-byte unit (pi, t, c) at pi * 128 + 8 t + (c ^ (t >> 1)), pi
-    // counted inside the staged part (the XOR keeps both the writes and the reads free of bank
-    // conflicts). A wave reuses its stage for the next pair after reading it (LDS accesses of
-    // one wave complete in order).
-    static_assert(U % 2 == 0, "x loads move pairs of k-steps");
-    const int lr = lane >> 3, lc = lane & 7;
-    const XT *lrow[2];
-#pragma unroll
-    for (int eta = 0; eta < 2; ++eta) {
-        const int64_t lm = ((int64_t)mt * tgw + tgi) * 16 + 8 * eta + lr;
-        lrow[eta] = static_cast<const XT *>(a.x) + (b * a.seq + (lm < a.seq ? lm : a.seq - 1)) * a.d_in +
-                    (lc & 3) * EV;
-    }
-    const XT *dummy = static_cast<const XT *>(a.x);
-    constexpr int SL = kStageLoads < U ? kStageLoads : U;   // loads staged at a time
-    char *stage = smem + a.stage_off + wave * (SL * 1024);
-    struct Batch {
-        XV x[U];
-    };
-    auto load_batch = [&](Batch &bt, const Desc &d) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int st = 2 * (j >> 1) + (lc >> 2);    // step of this lane's chunk inside the batch
-            bt.x[j] = stream_load<XV, XNT>(
-                reinterpret_cast<const XV *>(st < d.n ? lrow[j & 1] + (int64_t)KSTEP * (d.s0 + st) : dummy));
-        }
-    };
-    // loads [m SL, (m + 1) SL) of a batch (steps of the same range) pass through the stage together
-    auto stage_batch = [&](const Batch &bt, int m) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = m * SL; j < (m + 1) * SL; ++j) {
-            const int t = 8 * (j & 1) + lr;
-            *reinterpret_cast<XV *>(stage + (((j - m * SL) >> 1) * 128 + 8 * t + (lc ^ (t >> 1))) * 16) = bt.x[j];
-        }
-    };
-    auto staged = [&](int u, int m) __attribute__((always_inline)) -> XV {
-        const int c = 4 * (u & 1) + gq;
-        return *reinterpret_cast<const XV *>(stage + (((u - m * SL) >> 1) * 128 + 8 * r16 + (c ^ (r16 >> 1))) * 16);
-    };
-    f32x4 acc[GM];
-#pragma unroll
-    for (int g = 0; g < GM; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto compute_chunk = [&](const Batch &bt, const Desc &d, const XT *reg, int sp, int m) __attribute__((always_inline)) {
-        stage_batch(bt, m);
-        XV xv[SL];
-#pragma unroll
-        for (int v = 0; v < SL; ++v)
-            if (m * SL + v < d.n) xv[v] = staged(m * SL + v, m);
-        XV av[SL][GM];
-#pragma unroll
-        for (int v = 0; v < SL; ++v)
-#pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                const int u = m * SL + v;
-                const XT *ap;
-                if constexpr (SRC != SRC_DENSE)
-                    ap = reg + g * 16 * a.arow + (kBf16 ? ((sp + u) >> 1) * 16 + 8 * (gq & 1) : ((sp + u) >> 2) * 16 + 4 * gq);
-                else
-                    ap = reg + g * 16 * a.arow + (sp + u) * KSTEP + (kBf16 ? 8 : 4) * gq;
-                if (u < d.n) av[v][g] = *reinterpret_cast<const XV *>(ap);
-            }
-#pragma unroll
-        for (int v = 0; v < SL; ++v) {
-            if (m * SL + v >= d.n) break;
-#pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                if constexpr (kBf16) {
-                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[v][g], xv[v], acc[g], 0, 0, 0);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[v][g][e], xv[v][e], acc[g], 0, 0, 0);
-                }
-            }
-        }
-    };
-
-    auto compute_batch = [&](const Batch &bt, const Desc &d) __attribute__((always_inline)) {
-        const XT *reg = ring + (d.g & 1) * a.region + r16 * a.arow;
-        const int sp = d.s0 - d.g * pb * SPB;    // step inside the piece
-#pragma unroll
-        for (int m = 0; m < U / SL; ++m) {
-            if (m * SL >= d.n) break;
-            compute_chunk(bt, d, reg, sp, m);
-        }
-    };
-
-    // ---- prologue: index loads of pieces 0 and 1, then x of the first two batches; the
-    // decode below waits for its own loads only (loads complete in order).
-    RawIdx raw[kFillBatch];
-    {
-        RawIdx raw1[kFillBatch];
-        if constexpr (SRC != SRC_DENSE) {
-            idx_load(0, raw);
-            idx_load(1, raw1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        Cur cur{0, 0, 0};
-        share(cur);
-        skip_empty(cur);
-        Desc da = next(cur), db = next(cur);
-        Batch ba, bb;
-        load_batch(ba, da);
-        load_batch(bb, db);
-        if constexpr (SRC != SRC_DENSE) {
-            __syncthreads();    // the value table staged by lane 0 is visible to every wave
-            idx_store(0, raw);
-            idx_store(1, raw1);
-            idx_load(2, raw);
-        } else {
-            dense_fill(0);
-            dense_fill(1);
-        }
-        __syncthreads();
-
-        // ---- main loop. Entering piece g + 1 from g: barrier (all waves are done with piece
-        // g, and piece g + 1 is complete), then piece g + 2 is filled into piece g's region.
-        int pg = 0;
-        auto enter = [&](int g) __attribute__((always_inline)) {
-            while (pg < g) {
-                __syncthreads();
-                if constexpr (SRC != SRC_DENSE) {
-                    idx_store(pg + 2, raw);
-                    idx_load(pg + 3, raw);
-                } else {
-                    dense_fill(pg + 2);
-                }
-                ++pg;
-            }
-        };
-        // batch i sits in ba (i even) or bb (i odd); batch i + 1 is in flight in the other
-        while (da.n > 0) {
-            enter(da.g);
-            compute_batch(ba, da);
-            da = next(cur);
-            load_batch(ba, da);
-            __builtin_amdgcn_sched_barrier(0);    // keep the refill ahead of the next MFMAs
-            if (db.n == 0) break;
-            enter(db.g);
-            compute_batch(bb, db);
-            db = next(cur);
-            load_batch(bb, db);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        enter(npiece - 1);    // every wave passes the same npiece - 1 boundaries
-    }
-
-    // acc[g][e]: token r16, rank 4*gq + e of group g, summed over this wave's k range
-    if (ks > 1) {
-#pragma unroll
-        for (int g = 0; g < GM; ++g) *reinterpret_cast<f32x4 *>(red + ((wave * GM + g) * 64 + lane) * 4) = acc[g];
-        __syncthreads();
-        if (ksi != 0) return;
-#pragma unroll
-        for (int g = 0; g < GM; ++g) {
-            f32x4 sum = *reinterpret_cast<const f32x4 *>(red + ((tgi * GM + g) * 64 + lane) * 4);
-            for (int k2 = 1; k2 < ks; ++k2)
-                sum += *reinterpret_cast<const f32x4 *>(red + (((k2 * tgw + tgi) * GM + g) * 64 + lane) * 4);
-            acc[g] = sum;
-        }
-    }
-    if (!valid) return;
-    const float ms_b = a.mid_scale ? a.mid_scale[b] : 1.0f;
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        if (gs[g] < 0) continue;
-        XT *dst = static_cast<XT *>(a.mid) + row * a.MR + (mod * a.G + g) * 16 + 4 * gq;
-        if constexpr (kBf16) {
-            bf16x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (__bf16)(acc[g][e] * ms_b);
-            *reinterpret_cast<bf16x4 *>(dst) = o;
-        } else {
-            *reinterpret_cast<f32x4 *>(dst) = acc[g] * ms_b;
-        }
-    }
-}
-
-// ============================================================================ expand
-template <typename YT>
-__device__ __forceinline__ float finish(float acc, float s, float yold, bool accumulate) {
-    const float d = DT<YT>::round(DT<YT>::round(acc) * s);
-    return accumulate ? DT<YT>::round(yold + d) : d;
-}
-
-// y vector of 8 consecutive outputs (16 B for bf16, 32 B for fp32).
-template <typename YT> struct Y8;
-template <> struct Y8<__bf16> {
-    bf16x8 v;
-    __device__ __forceinline__ void load(const __bf16 *p) { v = stream_load(reinterpret_cast<const bf16x8 *>(p)); }
-    __device__ __forceinline__ void store(__bf16 *p) const { stream_store(reinterpret_cast<bf16x8 *>(p), v); }
-    __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
-    __device__ __forceinline__ void set(int e, float f) { v[e] = (__bf16)f; }
-};
-template <> struct Y8<float> {
-    f32x4 lo, hi;
-    __device__ __forceinline__ void load(const float *p) {
-        lo = stream_load(reinterpret_cast<const f32x4 *>(p));
-        hi = stream_load(reinterpret_cast<const f32x4 *>(p + 4));
-    }
-    __device__ __forceinline__ void store(float *p) const {
-        stream_store(reinterpret_cast<f32x4 *>(p), lo);
-        stream_store(reinterpret_cast<f32x4 *>(p + 4), hi);
-    }
-    __device__ __forceinline__ float get(int e) const { return e < 4 ? lo[e] : hi[e - 4]; }
-    __device__ __forceinline__ void set(int e, float f) {
-        if (e < 4) lo[e] = f;
-        else hi[e - 4] = f;
-    }
-};
-
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
-__device__ __forceinline__ void expand_body(const LoraArgs &a) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    // bf16 y with output tiles of whole lines: the whole-line y path (line_subtile below)
-    constexpr bool LINE = sizeof(YT) == 2 && BOM % 64 == 0;
-    typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
-    const int o_tiles = (int)((a.d_out + a.BO - 1) / a.BO);
-    const int64_t obase = (int64_t)(blockIdx.x % o_tiles) * a.BO;
-    const int tile = blockIdx.x / o_tiles;
-    const int64_t b = tile / a.tiles_e;
-    const int mt = tile % a.tiles_e;
-    const float s_b = a.out_scale_vec ? a.out_scale_vec[b] : a.out_scale;
-
-    int64_t gslot[GM];
-    bool any = false;
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        gslot[g] = g < a.G ? route_slot(a, b, g / a.n_rg, false) : -1;
-        any = any || gslot[g] >= 0;
-    }
-    auto sub_row = [&](int sub, bool &valid) __attribute__((always_inline)) -> int64_t {
-        const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + r16;
-        valid = m < a.seq;
-        return b * a.seq + (valid ? m : a.seq - 1);
-    };
-    if (!any) {
-        if (ACC) return;
-        // Empty route in write mode: the delta is zero.
-        for (int sub = 0; sub < a.subs_e; ++sub) {
-            bool valid;
-            const int64_t row = sub_row(sub, valid);
-            if (!valid) continue;
-            YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
-            for (int o = gq; o < a.BO; o += 4)
-                if (obase + o < a.d_out) yr[obase + o] = DT<YT>::from_f32(0.0f);
-        }
-        return;
-    }
-
-    constexpr int NP = BOM / 32;
-    const int np = a.BO / 32;
-
-    // Whole-line y path (bf16 y): rows of this wave's two 8-token halves of sub-tile `sub`, and
-    // its y loads (access j: token 8 (j & 1) + lane / 8, outputs 64 (j >> 1) + 8 (lane % 8) ..).
-    // They are issued per sub-tile, after the B tile is built. Issued earlier they cost the
-    // sweep 1.8 % ahead of the B index loads (the decode waits behind them: loads complete in
-    // order) and 2.6 % right behind them (the decode does not wait, but the tile's y registers
-    // stay live through the decode and the barrier).
-    constexpr int NJ = BOM / 32;
-    const int64_t omax = a.d_out - 8;
-    auto line_rows = [&](int sub, int64_t *lrow, bool *lval) __attribute__((always_inline)) {
-#pragma unroll
-        for (int eta = 0; eta < 2; ++eta) {
-            const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + 8 * eta + (lane >> 3);
-            lval[eta] = m < a.seq;
-            lrow[eta] = (b * a.seq + (lval[eta] ? m : a.seq - 1)) * a.d_out;
-        }
-    };
-    auto line_load = [&](int sub, bf16x8 *yv) __attribute__((always_inline)) {
-        int64_t lrow[2];
-        bool lval[2];
-        line_rows(sub, lrow, lval);
-        const __bf16 *yb = static_cast<const __bf16 *>(a.y);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-            yv[j] = stream_load<bf16x8, true>(reinterpret_cast<const bf16x8 *>(
-                yb + lrow[j & 1] + std::min<int64_t>(obase + 64 * (j >> 1) + 8 * (lane & 7), omax)));
-    };
-
-    // mid fragments; groups without an adapter read group 0 of the same row (their B
-    // fragments are zero), so every lane issues the same unconditional loads.
-    int gsrc[GM];
-#pragma unroll
-    for (int g = 0; g < GM; ++g) gsrc[g] = gslot[g] >= 0 ? g : 0;
-
-    // Per-route B multipliers (scalar loads: b and the route are uniform). Route j's first
-    // rank group is g = j * n_rg.
-    float gw[GM], gsc[GM];
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        const int j = (g < a.G ? g : 0) / a.n_rg;
-        gw[g] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
-        gsc[g] = (gslot[g] >= 0 && a.s_scale) ? a.s_scale[gslot[g]] : 1.0f;
-    }
-    auto route_pick = [&](int j, int64_t &slot, float &w, float &sc) __attribute__((always_inline)) {
-        const int g0 = j * a.n_rg;
-        slot = gslot[0];
-        w = gw[0];
-        sc = gsc[0];
-#pragma unroll
-        for (int q = 1; q < GM; ++q) {
-            slot = g0 == q ? gslot[q] : slot;
-            w = g0 == q ? gw[q] : w;
-            sc = g0 == q ? gsc[q] : sc;
-        }
-    };
-
-    // ---- B tile of this output range into LDS (bp), read from there by every MFMA.
-    // Indexed: the 16-value periods of blocks [blk_lo, blk_lo + nblk) of every route entry,
-    // one item per quarter period (4 values), 2 items per thread per batch.
-    // Dense: rows o in [obase, o_end) of every route entry's B, (route, o - obase, rank).
-    float *lut = reinterpret_cast<float *>(smem);
-    XT *bp = reinterpret_cast<XT *>(smem + kHead);
-    const int64_t blk_lo = (obase * a.rank) >> 6;
-    const int64_t o_end = std::min<int64_t>(obase + a.BO, a.d_out);
-    if constexpr (SRC != SRC_DENSE) {
-        const int per_route = (int)(((o_end * a.rank + kBlock - 1) >> 6) - blk_lo) * 4;
-        const int items = a.n_route * per_route;
-        RawIdx raw[2];
-        // block of item `it` inside the factor; 0 if its route entry is empty
-        auto dec_block = [&](int it, int64_t &slot, float &w, float &sc) __attribute__((always_inline)) -> int64_t {
-            const int j = a.n_route == 1 ? 0 : it / per_route;
-            route_pick(j, slot, w, sc);
-            const int64_t blk = blk_lo + ((it - j * per_route) >> 2);
-            return slot >= 0 ? blk : 0;
-        };
-        auto dec_load = [&](int base) __attribute__((always_inline)) {
-            int64_t slot[2], blk[2];
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                float w, sc;
-                blk[q] = dec_block(std::min(base + q * kThreads + tid, items - 1), slot[q], w, sc);
-                slot[q] = slot[q] >= 0 ? slot[q] : 0;
-            }
-            load_raw<2, SRC == SRC_PACKED, fixed_levels<SRC>()>(a.b_src, slot, blk, raw);
-        };
-        auto dec_store = [&](int base) __attribute__((always_inline)) {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int it = base + q * kThreads + tid;
-                if (it >= items) break;
-                const int j = a.n_route == 1 ? 0 : it / per_route;
-                const int rem = it - j * per_route;
-                const int blk = rem >> 2, qt = rem & 3;
-                int64_t slot;
-                float w, sc;
-                uint32_t k[kMaxLevels];
-                const bool ok = extract_indices<SRC == SRC_PACKED, fixed_levels<SRC>()>(a.b_src, dec_block(it, slot, w, sc), raw[q], k);
-                const bool live = slot >= 0;
-                if (live && !ok) record_error(a.err, kErrIndex);
-                XT *dst = bp + ((int64_t)j * a.nblk_max + blk) * 16 + 4 * qt;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float d = (decode_value<fixed_levels<SRC>()>(lut, a.b_src.levels, k, sign_mask_rt(4 * qt + e)) * sc) * w;
-                    v[e] = live ? d : 0.0f;
-                }
-                if constexpr (sizeof(XT) == 2) {
-                    bf16x4 pk;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) pk[e] = (__bf16)v[e];
-                    *reinterpret_cast<bf16x4 *>(dst) = pk;
-                } else {
-                    *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-                }
-            }
-        };
-        dec_load(0);
-        stage_lut(lut, a.luts.v[1][0], tid);
-        __syncthreads();
-        dec_store(0);
-        for (int base = 2 * kThreads; base < items; base += 2 * kThreads) {
-            dec_load(base);
-            dec_store(base);
-        }
-    } else {
-        // 16-byte vectors of (o_end - obase) * rank consecutive values per route entry
-        constexpr int EV = 16 / sizeof(XT);
-        const int per_route = (int)((o_end - obase) * a.rank / EV);
-        const int items = a.n_route * per_route;
-        for (int it = tid; it < items; it += kThreads) {
-            const int j = it / per_route, c = it - j * per_route;
-            int64_t slot;
-            float w, sc;
-            route_pick(j, slot, w, sc);
-            f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (slot >= 0)
-                v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_b) +
-                                                     (slot * a.d_out + obase) * a.rank + (int64_t)c * EV);
-            *reinterpret_cast<f32x4 *>(bp + (int64_t)j * a.BO * a.rank + (int64_t)c * EV) = v;
-        }
-    }
-    __syncthreads();
-
-    // ---- B fragment (p, h, g) from LDS. MFMA (p, h) row i <-> output 32p + 8(i/4) + 4h + (i%4),
-    // so lane (token r16, group gq) ends with outputs 32p + 8gq .. +7 of its token. QUAD
-    // (rank % 4 == 0): the 4 ranks of a fragment are 4 consecutive LDS values, one 8-byte read
-    // (fp32: 16 bytes); dead fragments read a valid address and are zeroed, without branches.
-    auto b_index = [&](int j, int64_t o, int r) __attribute__((always_inline)) -> int64_t {
-        if constexpr (SRC != SRC_DENSE) {
-            const int64_t f = o * a.rank + r;
-            return ((int64_t)j * a.nblk_max + (f >> 6) - blk_lo) * 16 + (f & 15);
-        } else {
-            return ((int64_t)j * a.BO + (o - obase)) * a.rank + r;
-        }
-    };
-    auto bfrag = [&](int p, int h, int g) __attribute__((always_inline)) -> Frag {
-        const int64_t o = obase + 32 * p + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
-        const int gg = g < a.G ? g : 0;
-        const int j = gg / a.n_rg;
-        const int rr = (gg % a.n_rg) * 16 + 4 * gq;
-        const bool live = p < np && gslot[g] >= 0 && o < o_end && rr < a.rank;
-        Frag fr;
-        if constexpr (QUAD) {
-            fr = *reinterpret_cast<const Frag *>(bp + b_index(j, live ? o : obase, live ? rr : 0));
-            fr = live ? fr : Frag{};
-        } else {
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool le = live && rr + e < a.rank;
-                const float t = DT<XT>::to_f32(bp[b_index(j, le ? o : obase, le ? rr + e : 0)]);
-                v[e] = le ? t : 0.0f;
-            }
-            if constexpr (sizeof(XT) == 2) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) fr[e] = __builtin_bit_cast(short, (__bf16)v[e]);
-            } else {
-                fr = f32x4{v[0], v[1], v[2], v[3]};
-            }
-        }
-        return fr;
-    };
-    auto compute = [&](const Frag *mf, int p, float vals[8]) __attribute__((always_inline)) {
-        f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                // a group without an adapter contributes exact zeros (its mid slot is not written)
-                const Frag m = gslot[g] >= 0 ? mf[g] : Frag{};
-                const Frag bf = bfrag(p, h, g);
-                if constexpr (sizeof(XT) == 2) {
-                    acc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf, m, acc[h], 0, 0, 0);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[e], m[e], acc[h], 0, 0, 0);
-                }
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            vals[e] = acc[0][e];
-            vals[4 + e] = acc[1][e];
-        }
-    };
-
-    // ---- sub-tiles: 16 tokens per wave each. Every load of a sub-tile is issued up front
-    // (rows and columns clamped in range); waves of other workgroups hide the latency.
-
-    // Whole-line y path (bf16 y). The y tile of a wave (16 tokens x BOM outputs) moves in
-    // loads and stores that each cover whole 128-byte lines: access j gives lane L token
-    // 8 (j & 1) + L / 8 and outputs 64 (j >> 1) + 8 (L % 8) .. + 7, with the non-temporal hint
-    // (measured: +5 % read-modify-write bandwidth; split-line accesses lose with it). The
-    // delta d = round_y(round_y(acc) * s) is finished in the MFMA layout (lane: token r16,
-    // outputs 32 p + 8 gq ..) and exchanged through a per-wave LDS tile, HB outputs at a time
-    // (a 4 KB tile: the workgroup's LDS stays small enough for 8 workgroups per CU): 16-byte
-    // unit (token t, chunk q) at (HB / 8) t + (q ^ swz(t)), conflict-free for both sides at
-    // HB >= 128. A wave reuses its tile for the next half after reading it back (LDS accesses
-    // of one wave complete in order).
-    constexpr int HB = kExchangeOutputs < BOM ? kExchangeOutputs : BOM;   // outputs per exchange
-    auto line_subtile = [&](int sub, const Frag *mf, const bf16x8 *yv) __attribute__((always_inline)) {
-        __bf16 *stg = reinterpret_cast<__bf16 *>(smem + a.estage_off) + wave * 16 * HB;
-        constexpr int RU = HB / 8;     // 16-byte units per token row of the tile
-        auto unit = [&](int t, int q) __attribute__((always_inline)) {
-            const int swz = ((t & 7) | ((((t >> 3) ^ t) & 1) << 3)) & (RU - 1);
-            return stg + (RU * t + (q ^ swz)) * 8;
-        };
-        const int lr = lane >> 3, lc = lane & 7;
-        int64_t lrow[2];
-        bool lval[2];
-        line_rows(sub, lrow, lval);
-        __bf16 *yb = static_cast<__bf16 *>(a.y);
-        constexpr int PH = HB / 32;    // MFMA column groups (and y accesses) per exchange
-#pragma unroll
-        for (int h = 0; h < BOM / HB; ++h) {
-#pragma unroll
-            for (int p = h * PH; p < (h + 1) * PH; ++p) {
-                if (p >= np) break;
-                float vals[8];
-                compute(mf, p, vals);
-                bf16x8 d;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d[e] = (__bf16)(DT<YT>::round(vals[e]) * s_b);
-                *reinterpret_cast<bf16x8 *>(unit(r16, 4 * (p - h * PH) + gq)) = d;
-            }
-#pragma unroll
-            for (int j = h * PH; j < (h + 1) * PH; ++j) {
-                const int t = 8 * (j & 1) + lr, q = 8 * (j >> 1) + lc;
-                const bf16x8 d = *reinterpret_cast<const bf16x8 *>(unit(t, q - h * RU));
-                const int64_t o8 = obase + 8 * q;
-                bf16x8 out;
-                if constexpr (ACC) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) out[e] = (__bf16)((float)yv[j][e] + (float)d[e]);
-                } else {
-                    out = d;
-                }
-                if (lval[j & 1] && 8 * q < a.BO && o8 < a.d_out)
-                    stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + lrow[j & 1] + o8), out);
-            }
-        }
-    };
-    for (int sub = 0; sub < a.subs_e; ++sub) {
-        // keeps the B fragment reads inside the loop (read from LDS per use, not held in registers)
-        asm volatile("" ::: "memory");
-        bool valid;
-        const int64_t row = sub_row(sub, valid);
-        Frag mf[GM];
-#pragma unroll
-        for (int g = 0; g < GM; ++g) {
-            const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + (a.mid_goff + gsrc[g]) * 16 + 4 * gq;
-            if constexpr (sizeof(XT) == 2) mf[g] = *reinterpret_cast<const i16x4 *>(src);
-            else mf[g] = *reinterpret_cast<const f32x4 *>(src);
-        }
-        YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
-        if constexpr (LINE) {
-            if (a.vec_y) {
-                bf16x8 yv[NJ];
-                if (ACC) line_load(sub, yv);
-                line_subtile(sub, mf, yv);
-                continue;
-            }
-        }
-        if (a.vec_y) {
-            Y8<YT> yv[NP];
-            if constexpr (ACC) {
-#pragma unroll
-                for (int p = 0; p < NP; ++p)
-                    if (p < np) yv[p].load(yr + std::min<int64_t>(obase + 32 * p + 8 * gq, omax));
-            }
-#pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                if (p >= np) break;
-                float vals[8];
-                compute(mf, p, vals);
-                const int64_t o8 = obase + 32 * p + 8 * gq;
-                Y8<YT> out;
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    out.set(e, finish<YT>(vals[e], s_b, ACC ? yv[p].get(e) : 0.0f, ACC));
-                if (valid && o8 < a.d_out) out.store(yr + o8);
-            }
-        } else {
-            // element path for d_out not a multiple of 8 (rows not 16-byte aligned)
-            for (int p = 0; p < np; ++p) {
-                float vals[8];
-                compute(mf, p, vals);
-                const int64_t o8 = obase + 32 * p + 8 * gq;
-                if (!valid) continue;
-                for (int e = 0; e < 8; ++e) {
-                    if (o8 + e >= a.d_out) break;
-                    const float yo = ACC ? DT<YT>::to_f32(yr[o8 + e]) : 0.0f;
-                    yr[o8 + e] = DT<YT>::from_f32(finish<YT>(vals[e], s_b, yo, ACC));
-                }
-            }
-        }
-    }
-}
-
-// Two entry points of one body: the second asks the compiler for 4 waves per SIMD (at most
-// 128 VGPRs); it is used where the body fits that budget without spilling (one rank group,
-// bf16 output).
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
-__global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a);
-}
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) expand_kernel_w4(LoraArgs a) {
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a);
-}
 
 // ============================================================================ host plan
 int env_int(const char *name, int dflt) {
@@ -980,13 +14,6 @@ int env_int(const char *name, int dflt) {
     return x > 0 ? x : dflt;
 }
 
-struct Plan {
-    int G, n_rg, GM, MR;
-    int tiles_s, ks, pb, arow, region, red_off, stage_off;
-    size_t lds_s, lds_e;
-    int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off;
-    int64_t off_mid, total;
-};
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
@@ -1069,70 +96,6 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     return p;
 }
 
-#ifndef LITHE_SHARED_X_NT
-#define LITHE_SHARED_X_NT 0
-#endif
-
-template <typename XT, int SRC, int GM>
-void launch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    if constexpr (SRC != SRC_DENSE && !LITHE_SHARED_X_NT) {
-        if (a.n_mod_wg > 1) {    // replicated shared-input shrink: x stays in L2 for the other modules
-            hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU, false>),
-                               dim3((unsigned)((a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg)), dim3(kThreads),
-                               p.lds_s, st, a);
-            return;
-        }
-    }
-    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU, true>),
-                       dim3((unsigned)(a.n_mod_wg > 1 ? (a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg
-                                                      : a.n_batch * p.tiles_s)),
-                       dim3(kThreads), p.lds_s, st, a);
-}
-
-template <typename XT, typename YT, int SRC, int GM, int BOM>
-void launch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    dim3 ge((unsigned)(((a.d_out + p.BO - 1) / p.BO) * a.n_batch * p.tiles_e));
-    const bool quad = (a.rank & 3) == 0;
-    if constexpr (GM == 1 && sizeof(YT) == 2) {
-        if (quad) {
-            if (a.accumulate)
-                hipLaunchKernelGGL((expand_kernel_w4<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), p.lds_e, st, a);
-            else
-                hipLaunchKernelGGL((expand_kernel_w4<XT, YT, SRC, GM, BOM, false, true>), ge, dim3(kThreads), p.lds_e, st, a);
-            return;
-        }
-    }
-    if (a.accumulate) {
-        if (quad) hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), p.lds_e, st, a);
-        else hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, false>), ge, dim3(kThreads), p.lds_e, st, a);
-    } else {
-        if (quad) hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false, true>), ge, dim3(kThreads), p.lds_e, st, a);
-        else hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false, false>), ge, dim3(kThreads), p.lds_e, st, a);
-    }
-}
-
-template <typename XT, int SRC>
-void dispatch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    switch (p.GM) {
-        case 1: launch_shrink<XT, SRC, 1>(p, a, st); break;
-        case 2: launch_shrink<XT, SRC, 2>(p, a, st); break;
-        case 4: launch_shrink<XT, SRC, 4>(p, a, st); break;
-        default: launch_shrink<XT, SRC, 8>(p, a, st); break;
-    }
-}
-
-// expand output tiles: BOM outputs per workgroup (make_plan's bo_max for the same GM)
-template <typename XT, typename YT, int SRC>
-void dispatch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    constexpr bool bf = sizeof(XT) == 2;
-    switch (p.GM) {
-        case 1: launch_expand<XT, YT, SRC, 1, bf ? 256 : 128>(p, a, st); break;
-        case 2: launch_expand<XT, YT, SRC, 2, bf ? 256 : 128>(p, a, st); break;
-        case 4: launch_expand<XT, YT, SRC, 4, bf ? 128 : 64>(p, a, st); break;
-        default: launch_expand<XT, YT, SRC, 8, bf ? 64 : 32>(p, a, st); break;
-    }
-}
-
 int src_of(const LoraArgs &a, int kind) {
     if (kind == LITHE_FACTOR_DENSE) return SRC_DENSE;
     if (a.a_src.kind == LITHE_IDX_PACKED9 && a.b_src.kind == LITHE_IDX_PACKED9 && a.a_src.levels == kPackedLevels)
@@ -1140,26 +103,17 @@ int src_of(const LoraArgs &a, int kind) {
     return SRC_INDEXED;
 }
 
-template <typename XT, typename YT>
-void dispatch(bool shrink, const Plan &p, const LoraArgs &a, int src, hipStream_t st) {
-    if (shrink) {
-        if (src == SRC_DENSE) dispatch_shrink<XT, SRC_DENSE>(p, a, st);
-        else if (src == SRC_PACKED) dispatch_shrink<XT, SRC_PACKED>(p, a, st);
-        else dispatch_shrink<XT, SRC_INDEXED>(p, a, st);
-    } else {
-        if (src == SRC_DENSE) dispatch_expand<XT, YT, SRC_DENSE>(p, a, st);
-        else if (src == SRC_PACKED) dispatch_expand<XT, YT, SRC_PACKED>(p, a, st);
-        else dispatch_expand<XT, YT, SRC_INDEXED>(p, a, st);
-    }
-}
-
 void launch_typed(bool shrink, int x_dtype, int y_dtype, const Plan &p, const LoraArgs &a, int src, hipStream_t st) {
-    if (x_dtype == LITHE_DT_BF16) {
-        if (y_dtype == LITHE_DT_BF16) dispatch<__bf16, __bf16>(shrink, p, a, src, st);
-        else dispatch<__bf16, float>(shrink, p, a, src, st);
+    const bool xb = x_dtype == LITHE_DT_BF16, yb = y_dtype == LITHE_DT_BF16;
+    if (shrink) {
+        if (xb) launch_shrink_bf16(p, a, src, st);
+        else launch_shrink_f32(p, a, src, st);
+    } else if (xb) {
+        if (yb) launch_expand_bf16_bf16(p, a, src, st);
+        else launch_expand_bf16_f32(p, a, src, st);
     } else {
-        if (y_dtype == LITHE_DT_BF16) dispatch<float, __bf16>(shrink, p, a, src, st);
-        else dispatch<float, float>(shrink, p, a, src, st);
+        if (yb) launch_expand_f32_bf16(p, a, src, st);
+        else launch_expand_f32_f32(p, a, src, st);
     }
 }
 

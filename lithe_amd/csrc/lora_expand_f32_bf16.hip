@@ -1,0 +1,13 @@
+// Expand kernels for fp32 activations and bf16 outputs (one translation unit per dtype pair:
+// parallel builds).
+#include "lora_kernels.h"
+
+namespace lithe {
+
+void launch_expand_f32_bf16(const Plan &p, const LoraArgs &a, int src, hipStream_t st) {
+    if (src == SRC_DENSE) dispatch_expand<float, __bf16, SRC_DENSE>(p, a, st);
+    else if (src == SRC_PACKED) dispatch_expand<float, __bf16, SRC_PACKED>(p, a, st);
+    else dispatch_expand<float, __bf16, SRC_INDEXED>(p, a, st);
+}
+
+}  // namespace lithe

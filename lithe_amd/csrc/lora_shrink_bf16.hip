@@ -1,0 +1,12 @@
+// Shrink kernels for bf16 activations (one translation unit per dtype: parallel builds).
+#include "lora_kernels.h"
+
+namespace lithe {
+
+void launch_shrink_bf16(const Plan &p, const LoraArgs &a, int src, hipStream_t st) {
+    if (src == SRC_DENSE) dispatch_shrink<__bf16, SRC_DENSE>(p, a, st);
+    else if (src == SRC_PACKED) dispatch_shrink<__bf16, SRC_PACKED>(p, a, st);
+    else dispatch_shrink<__bf16, SRC_INDEXED>(p, a, st);
+}
+
+}  // namespace lithe
