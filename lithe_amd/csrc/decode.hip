@@ -153,32 +153,26 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 }
 
 // Packed 3-level fast path of the bulk decode (the resident bank of the twin codebook). Each
-// thread owns ITER half-blocks of one selected slot, spaced kThreads apart, and issues the
-// index loads of all of them before decoding the first, so a wave keeps ITER round trips in
-// flight instead of one; the workgroup count drops ITER-fold. Output order and values are
-// those of decode_kernel.
-// Side bytes and layout size. A side table that stays in L2 (at most kStageSidesBlocks bytes,
-// half of one XCD's L2) is read with one byte load per half-block, issued after the index loads,
-// with 8 half-blocks per thread. A larger one is evicted by the output stream between uses: a
-// workgroup (SPAN consecutive blocks from blockIdx.x * SPAN) then reads its sides with coalesced
-// 4-byte loads issued after the index loads and takes them from LDS, and each thread owns 16
-// half-blocks (measured at rank 64, 2.8 MB of sides: 3.95 -> 4.19 TB/s from the staging, -> 4.47
-// with 16 half-blocks; at rank 16, 0.7 MB, the staged form is 3 % slower and 16 half-blocks gain
-// 0.3 %). In both forms every wave finishes its loads before its first store (stores that start
-// while a workgroup's index loads are landing cost 6 % at rank 16). The last workgroup of a
-// selection, or a side table not 4-byte aligned, reads the bytes one by one.
-constexpr int64_t kStageSidesBlocks = int64_t(1) << 21;
-constexpr int decode_iter(bool stage) { return stage ? 16 : 8; }
-template <typename OutT, bool STAGE>
+// thread owns kDecodeIter half-blocks of one selected slot, spaced kThreads apart, and issues
+// the index loads of all of them before decoding the first, so a wave keeps kDecodeIter round
+// trips in flight instead of one. Output order and values are those of decode_kernel.
+// Side bytes: a workgroup (SPAN consecutive blocks from blockIdx.x * SPAN) reads its sides with
+// coalesced 4-byte loads issued after the index loads and takes them from LDS; each thread owns
+// 16 half-blocks. Measured against one byte load per half-block and 8 half-blocks per thread:
+// rank 16 (0.7 MB of sides) 4.57 -> 4.70 TB/s, rank 64 (2.8 MB) 3.95 -> 4.45 TB/s; the staging
+// alone at 8 half-blocks lost 3 % at rank 16. Every wave finishes its loads before its first
+// store (stores that start while a workgroup's index loads are landing cost 6 % at rank 16). The
+// last workgroup of a selection, or a side table not 4-byte aligned, reads the bytes one by one.
+constexpr int kDecodeIter = 16;
+template <typename OutT>
 __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) {
-    constexpr int kDecodeIter = decode_iter(STAGE);
     constexpr int SPAN = kThreads * kDecodeIter / 2;
     static_assert(SPAN % (4 * kThreads) == 0, "whole 4-byte side loads per thread");
     __shared__ float lut[2 * kMaxLevels * 10];
-    __shared__ int8_t wg_side[STAGE ? SPAN : 4];
+    __shared__ int8_t wg_side[SPAN];
     if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
     const int64_t b0 = (int64_t)blockIdx.x * SPAN;
-    const bool whole = STAGE && a.sides && b0 + SPAN <= a.n_blocks &&
+    const bool whole = a.sides && b0 + SPAN <= a.n_blocks &&
                        (reinterpret_cast<uintptr_t>(a.sides) & 3u) == 0;
 
     const int sel = blockIdx.y;
@@ -199,7 +193,7 @@ __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) 
         sl[i] = bad ? 0 : slot;
     }
     load_raw<kDecodeIter, true, 3>(a.src, sl, blk, raw);
-    if (STAGE && whole) {
+    if (whole) {
         uint32_t sw[SPAN / (4 * kThreads)];
 #pragma unroll
         for (int q = 0; q < SPAN / (4 * kThreads); ++q)
@@ -221,9 +215,7 @@ __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) 
         const int h = (int)(hf & 1);
         uint32_t k[kMaxLevels];
         extract_indices<true, 3>(a.src, blk[i], raw[i], k);
-        int sd;
-        if constexpr (STAGE) sd = whole ? wg_side[blk[i] - b0] : side[i];
-        else sd = side[i];
+        const int sd = whole ? wg_side[blk[i] - b0] : side[i];
         const float *tab = lut + sd * kMaxLevels * 10;
         float v[8];
 #pragma unroll
@@ -373,16 +365,12 @@ static int32_t decode_impl(const lithe_index_src *src, const int32_t *slots, int
     // the widest grid is the one-half-block-per-thread kernel's
     if ((halves + kThreads - 1) / kThreads > kMaxGridX || n_sel > kMaxGridY) return LITHE_ERR_SHAPE;
     if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3) {
-        const bool stage = n_blocks > kStageSidesBlocks;
-        const int64_t per_wg = (int64_t)kThreads * decode_iter(stage);
+        const int64_t per_wg = (int64_t)kThreads * kDecodeIter;
         dim3 grid((unsigned)((halves + per_wg - 1) / per_wg), (unsigned)n_sel);
-        if (out_dtype == LITHE_DT_BF16) {
-            if (stage) hipLaunchKernelGGL((decode_packed3_kernel<__bf16, true>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);
-            else hipLaunchKernelGGL((decode_packed3_kernel<__bf16, false>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);
-        } else {
-            if (stage) hipLaunchKernelGGL((decode_packed3_kernel<float, true>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);
-            else hipLaunchKernelGGL((decode_packed3_kernel<float, false>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);
-        }
+        if (out_dtype == LITHE_DT_BF16)
+            hipLaunchKernelGGL(decode_packed3_kernel<__bf16>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(decode_packed3_kernel<float>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
         return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
     }
     dim3 grid((unsigned)((halves + kThreads - 1) / kThreads), (unsigned)n_sel);

@@ -164,17 +164,17 @@ def test_decode_bad_slot_zero_fills_and_flags():
 
 
 def test_decode_side_table_unaligned_and_tail():
-    """Layouts of more than 2**21 blocks read a workgroup's side bytes with 4-byte loads
-    where they can; a side table at an odd address and the partial last workgroup take the byte
-    path. Both forms give the oracle's bits: a small layout (2,058 blocks, byte path throughout)
-    at an aligned and an odd address here; the rank-64 FLUX layout in the next test."""
+    """The packed decode reads a workgroup's 2,048 side bytes with 4-byte loads where it can; a
+    side table at an odd address and the partial last workgroup take the byte path. Both forms
+    give the oracle's bits: a layout of 2,058 blocks (one whole workgroup and a tail) at an
+    aligned and an odd address here; the rank-64 FLUX layout in the next test."""
     from lithe_amd.kernels import _delta
     from lithe_amd.kernels.packed import _decode
     ad = random_adapter([("m0", 1024, 1024), ("m1", 1024, 2048), ("m2", 512, 2600)], rank=16, seed=4)
     _, bits, _ = _oracle_decode_bits(ad)
     words, layout = pack_adapter(ad)
     n = layout.total_blocks
-    assert n % 1024 != 0 and n > 2048
+    assert n % 2048 != 0 and n > 2048
     pa, pb = (p.cuda() for p in lithe_amd.twin_pools())
     w = words.cuda()
     aligned = decode_packed(w, layout, pa, pb)
@@ -190,15 +190,14 @@ def test_decode_side_table_unaligned_and_tail():
 
 
 def test_decode_rank64_flux_layout_staged_sides():
-    """The rank-64 FLUX layout plus one small module (2,801,768 blocks: side bytes through LDS,
-    and a partial last workgroup) against the C restatement, aligned and at an odd side-table
-    address."""
+    """The rank-64 FLUX layout plus one small module (2,801,768 blocks, a partial last
+    workgroup) against the C restatement, aligned and at an odd side-table address."""
     from lithe_amd.kernels import _delta
     from lithe_amd.kernels.packed import _decode
     ad = random_adapter(flux_modules() + [("extra", 64, 40)], rank=64, seed=12)
     words, layout = pack_adapter(ad)
     n = layout.total_blocks
-    assert n == 2_801_768 and n > 2 ** 21 and n % 1024 != 0
+    assert n == 2_801_768 and n % 2048 != 0
     pa, pb = ocb.twin_pools()
     ref_bits = native.decode(words.view(torch.int64).numpy().view(np.uint64), n, 3,
                              layout.sides.numpy(), pa, pb, want="bf16")
