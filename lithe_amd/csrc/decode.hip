@@ -158,12 +158,13 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 // trips in flight instead of one. Output order and values are those of decode_kernel.
 // Side bytes: a workgroup (SPAN consecutive blocks from blockIdx.x * SPAN) reads its sides with
 // coalesced 4-byte loads issued after the index loads and takes them from LDS; each thread owns
-// 16 half-blocks. Measured against one byte load per half-block and 8 half-blocks per thread:
-// rank 16 (0.7 MB of sides) 4.57 -> 4.70 TB/s, rank 64 (2.8 MB) 3.95 -> 4.45 TB/s; the staging
-// alone at 8 half-blocks lost 3 % at rank 16. Every wave finishes its loads before its first
+// 24 half-blocks (240 VGPRs, 2 waves per SIMD, no scratch). Measured against one byte load per
+// half-block and 8 half-blocks per thread: rank 16 (0.7 MB of sides) 4.57 -> 4.70 TB/s with 16
+// half-blocks, -> 4.81 with 24; rank 64 (2.8 MB) 3.95 -> 4.45 -> 4.66 TB/s; 32 half-blocks per
+// thread drop to 3.6 TB/s. The staging alone at 8 half-blocks lost 3 % at rank 16. Every wave finishes its loads before its first
 // store (stores that start while a workgroup's index loads are landing cost 6 % at rank 16). The
 // last workgroup of a selection, or a side table not 4-byte aligned, reads the bytes one by one.
-constexpr int kDecodeIter = 16;
+constexpr int kDecodeIter = 24;
 template <typename OutT>
 __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) {
     constexpr int SPAN = kThreads * kDecodeIter / 2;

@@ -164,17 +164,18 @@ def test_decode_bad_slot_zero_fills_and_flags():
 
 
 def test_decode_side_table_unaligned_and_tail():
-    """The packed decode reads a workgroup's 2,048 side bytes with 4-byte loads where it can; a
+    """The packed decode reads a workgroup's 3,072 side bytes with 4-byte loads where it can; a
     side table at an odd address and the partial last workgroup take the byte path. Both forms
-    give the oracle's bits: a layout of 2,058 blocks (one whole workgroup and a tail) at an
+    give the oracle's bits: a layout of 3,082 blocks (one whole workgroup and a tail) at an
     aligned and an odd address here; the rank-64 FLUX layout in the next test."""
     from lithe_amd.kernels import _delta
     from lithe_amd.kernels.packed import _decode
-    ad = random_adapter([("m0", 1024, 1024), ("m1", 1024, 2048), ("m2", 512, 2600)], rank=16, seed=4)
+    ad = random_adapter([("m0", 1024, 1024), ("m1", 1024, 2048), ("m2", 512, 2600), ("m3", 2048, 2048)], rank=16,
+                        seed=4)
     _, bits, _ = _oracle_decode_bits(ad)
     words, layout = pack_adapter(ad)
     n = layout.total_blocks
-    assert n % 2048 != 0 and n > 2048
+    assert n % 3072 != 0 and n > 3072
     pa, pb = (p.cuda() for p in lithe_amd.twin_pools())
     w = words.cuda()
     aligned = decode_packed(w, layout, pa, pb)
@@ -197,7 +198,7 @@ def test_decode_rank64_flux_layout_staged_sides():
     ad = random_adapter(flux_modules() + [("extra", 64, 40)], rank=64, seed=12)
     words, layout = pack_adapter(ad)
     n = layout.total_blocks
-    assert n == 2_801_768 and n % 2048 != 0
+    assert n == 2_801_768 and n % 3072 != 0
     pa, pb = ocb.twin_pools()
     ref_bits = native.decode(words.view(torch.int64).numpy().view(np.uint64), n, 3,
                              layout.sides.numpy(), pa, pb, want="bf16")
