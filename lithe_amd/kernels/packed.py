@@ -213,16 +213,23 @@ def blockify_factors(layout: PackedLayout, factors: Dict[str, Tuple[torch.Tensor
     if any(nxt < end for (_, end), (nxt, _) in zip(bounds, bounds[1:])):
         raise ValueError("layout offsets overlap")
     gaps = [nxt - end for (_, end), (nxt, _) in zip([(0, 0)] + bounds, bounds)]
-    zeros = torch.zeros(max(gaps), dtype=torch.float32, device=device)
-    parts = []
-    for (_, w), gap in zip(segs + [(None, None)], gaps):
-        if gap:
-            parts.append(zeros[:gap])
-        if w is not None:
-            parts.append(w.detach().reshape(-1).to(device=device, dtype=torch.float32))
-    out = torch.empty((layout.total_blocks, bs), dtype=torch.float32, device=device)
-    if parts:
-        torch.cat(parts, out=out.view(-1))
+    dev = torch.device(device)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    with torch.no_grad():    # no per-factor detach: nothing here is recorded for autograd
+        zeros = torch.zeros(max(gaps), dtype=torch.float32, device=dev)
+        parts = []
+        for (_, w), gap in zip(segs + [(None, None)], gaps):
+            if gap:
+                parts.append(zeros[:gap])
+            if w is not None:
+                flat = w.reshape(-1)
+                if flat.dtype != torch.float32 or flat.device != dev:
+                    flat = flat.to(device=dev, dtype=torch.float32)
+                parts.append(flat)
+        out = torch.empty((layout.total_blocks, bs), dtype=torch.float32, device=dev)
+        if parts:
+            torch.cat(parts, out=out.view(-1))
     return out
 
 
