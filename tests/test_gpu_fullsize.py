@@ -84,3 +84,30 @@ def test_fullsize_exact_properties(setup, name, d_in, d_out):
         want = odelta.shared_delta(rows, ia, opa, ib, opb, [0], RANK, d_out, SCALE)
         got = d[smp:smp + 1, :8].float().cpu().numpy()
         assert rel(got, want) < 2e-3, (name, smp)
+
+
+def test_fullsize_encode_round_trip():
+    """A whole 342-linear rank-16 adapter (700,416 blocks) decoded to dense factors and encoded
+    back into a bank slot (PackedBank.encode_factors): every B index comes back (pool B's level
+    scales are separable), and every A factor decodes to within 1e-7 of the original (equal A
+    scales admit other index triples with the same sum; tests/test_module.py:115-127 of the
+    reference)."""
+    import lithe_amd
+    from lithe_amd.kernels import pack_adapter, split_decoded
+    from helpers import flux_modules
+    ad = random_adapter(flux_modules(), rank=16, seed=77)
+    words, layout = pack_adapter(ad)
+    bank = PackedBank(layout, "cuda", capacity=2)
+    bank.add(words)
+    factors = lithe_amd.decode_factors(ad)                       # fp32 on the GPU
+    slot = bank.encode_factors(factors)
+    assert slot == 1 and bank.ingest_errors() == 0
+    got = bank.decode_slots(torch.tensor([slot], dtype=torch.int32, device="cuda"), dtype=torch.float32)[0]
+    got = split_decoded(got, layout)
+    from lithe_amd.kernels import unpack_indices
+    idx = unpack_indices(bank.words[slot], layout.num_indices).view(-1, 3).cpu().numpy()
+    for name, sa, sb, a_off, b_off in zip(layout.names, layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
+        nb = -(-sb[0] * sb[1] // 64)
+        assert np.array_equal(idx[b_off:b_off + nb].T, ad.indices[name]["B"].astype(np.int64)), name
+        a, _ = factors[name]
+        assert torch.allclose(got[name][0], a, atol=1e-7), name
