@@ -368,19 +368,32 @@ def decode_packed_stacked(bank: torch.Tensor, slots: torch.Tensor, layout: Packe
 
 
 def split_stacked(out: torch.Tensor, layout: PackedLayout, n_sel: int) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
-    """name -> (A (n_sel, r, d_in), B (n_sel, d_out, r)) views of a ``decode_packed_stacked`` buffer."""
-    flat = out.reshape(-1)
-    bs = layout.block_size
-    res = {}
-    for name, sa, sb, ao, bo in zip(layout.names, layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
-        na, nb = sa[0] * sa[1], sb[0] * sb[1]
-        nba, nbb = quant.num_blocks(sa, bs), quant.num_blocks(sb, bs)
-        if na != nba * bs or nb != nbb * bs:
-            raise ValueError(f"{name}: factors that do not fill whole blocks have no stacked view")
-        a = flat[n_sel * ao * bs: n_sel * (ao + nba) * bs].view(n_sel, sa[0], sa[1])
-        b = flat[n_sel * bo * bs: n_sel * (bo + nbb) * bs].view(n_sel, sb[0], sb[1])
-        res[name] = (a, b)
-    return res
+    """name -> (A (n_sel, r, d_in), B (n_sel, d_out, r)) views of a ``decode_packed_stacked`` buffer.
+
+    The factors lie back to back in residency order, so one ``split`` cuts every factor's
+    chunk; the sizes and shapes are computed once per layout and selection count."""
+    key = ("stacked_split", n_sel)
+    plan = layout._sides_dev.get(key)
+    if plan is None:
+        bs = layout.block_size
+        sizes, shapes, pos = [], [], 0
+        for name, sa, sb, ao, bo in zip(layout.names, layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
+            for shape, off in ((sa, ao), (sb, bo)):
+                n = shape[0] * shape[1]
+                nb = quant.num_blocks(shape, bs)
+                if n != nb * bs:
+                    raise ValueError(f"{name}: factors that do not fill whole blocks have no stacked view")
+                if off * bs != pos:
+                    raise ValueError("stacked views need the layout's factors back to back in residency order")
+                sizes.append(n_sel * n)
+                shapes.append((n_sel, shape[0], shape[1]))
+                pos += n
+        plan = (sizes, shapes, n_sel * pos)
+        layout._sides_dev[key] = plan
+    sizes, shapes, total = plan
+    chunks = out.reshape(-1)[:total].split(sizes)
+    return {name: (chunks[2 * i].view(shapes[2 * i]), chunks[2 * i + 1].view(shapes[2 * i + 1]))
+            for i, name in enumerate(layout.names)}
 
 
 def split_decoded(out: torch.Tensor, layout: PackedLayout) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
