@@ -397,11 +397,29 @@ def split_stacked(out: torch.Tensor, layout: PackedLayout, n_sel: int) -> Dict[s
 
 
 def split_decoded(out: torch.Tensor, layout: PackedLayout) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
-    """name -> (A (r, d_in), B (d_out, r)) as views into the decode output."""
-    flat = out.reshape(-1)
-    bs = layout.block_size
-    res = {}
-    for name, sa, sb, ao, bo in zip(layout.names, layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
-        na, nb = sa[0] * sa[1], sb[0] * sb[1]
-        res[name] = (flat[ao * bs: ao * bs + na].view(*sa), flat[bo * bs: bo * bs + nb].view(*sb))
-    return res
+    """name -> (A (r, d_in), B (d_out, r)) as views into the decode output (one ``split`` of the
+    flat output into factor chunks and block padding, computed once per layout)."""
+    key = "decoded_split"
+    plan = layout._sides_dev.get(key)
+    if plan is None:
+        bs = layout.block_size
+        segs = []
+        for sa, sb, ao, bo in zip(layout.shapes_a, layout.shapes_b, layout.a_off, layout.b_off):
+            segs += [(ao * bs, sa), (bo * bs, sb)]
+        order = sorted(range(len(segs)), key=lambda i: segs[i][0])
+        sizes, where, pos = [], [0] * len(segs), 0
+        for i in order:
+            off, shape = segs[i]
+            if off < pos:
+                raise ValueError("layout offsets overlap")
+            if off > pos:
+                sizes.append(off - pos)              # padding of the previous factor's last block
+            where[i] = len(sizes)
+            sizes.append(shape[0] * shape[1])
+            pos = off + shape[0] * shape[1]
+        plan = (sizes, where, [tuple(sh) for _, sh in segs], pos)
+        layout._sides_dev[key] = plan
+    sizes, where, shapes, total = plan
+    chunks = out.reshape(-1)[:total].split(sizes)
+    return {name: (chunks[where[2 * i]].view(shapes[2 * i]), chunks[where[2 * i + 1]].view(shapes[2 * i + 1]))
+            for i, name in enumerate(layout.names)}

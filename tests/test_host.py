@@ -145,3 +145,36 @@ def test_flux_target_count():
         names += [f"single_transformer_blocks.{i}.attn.{t}" for t in ("to_q", "to_k", "to_v")]
         names += [f"single_transformer_blocks.{i}.{t}" for t in ("proj_mlp", "proj_out", "norm.linear")]
     assert sum(module._match(n, module.FLUX_TARGET_MODULES) for n in names) == 342
+
+
+def test_split_views_equal_per_module_slices():
+    """split_decoded / split_stacked (one cached split of the flat buffer) give the same views as
+    slicing every factor at its layout offset, aliasing the buffer; stacked views refuse factors
+    that leave block padding."""
+    import pytest
+    import torch
+
+    from helpers import random_adapter
+    from lithe_amd.kernels import pack_adapter, split_decoded, split_stacked
+    ad = random_adapter([("a", 96, 40), ("odd", 7, 5), ("b", 128, 64)], rank=5, seed=1)
+    _, lay = pack_adapter(ad)
+    out = torch.arange(lay.total_blocks * 64, dtype=torch.float32).view(-1, 64)
+    flat = out.reshape(-1)
+    for _ in range(2):                                   # second call: the cached plan
+        got = split_decoded(out, lay)
+        for name, sa, sb, ao, bo in zip(lay.names, lay.shapes_a, lay.shapes_b, lay.a_off, lay.b_off):
+            na, nb = sa[0] * sa[1], sb[0] * sb[1]
+            assert torch.equal(got[name][0], flat[ao * 64: ao * 64 + na].view(*sa)), name
+            assert torch.equal(got[name][1], flat[bo * 64: bo * 64 + nb].view(*sb)), name
+            assert got[name][0].data_ptr() == flat[ao * 64:].data_ptr()
+    with pytest.raises(ValueError, match="whole blocks"):
+        split_stacked(out, lay, 2)
+    ad2 = random_adapter([("a", 128, 64), ("b", 256, 128)], rank=16, seed=2)
+    _, lay2 = pack_adapter(ad2)
+    n_sel = 3
+    buf = torch.arange(n_sel * lay2.total_blocks * 64, dtype=torch.float32)
+    st = split_stacked(buf, lay2, n_sel)
+    for name, sa, sb, ao, bo in zip(lay2.names, lay2.shapes_a, lay2.shapes_b, lay2.a_off, lay2.b_off):
+        na, nb = sa[0] * sa[1], sb[0] * sb[1]
+        assert torch.equal(st[name][0], buf[n_sel * ao * 64: n_sel * ao * 64 + n_sel * na].view(n_sel, *sa)), name
+        assert torch.equal(st[name][1], buf[n_sel * bo * 64: n_sel * bo * 64 + n_sel * nb].view(n_sel, *sb)), name
