@@ -631,6 +631,14 @@ def main():
         workload = "FLUX FFN pair 3072->12288->3072 at 512^2: B=14 x 1536 tokens, 1k-adapter packed bank"
 
     ms, graphed = time_sweeps(wl, args.steps, args.warmup, not args.no_graph)
+    # the kernels record bad slot ids and out-of-range indices in the workspace's error word
+    import ctypes
+    from lithe_amd.kernels import _hip
+    kflags = ctypes.c_int32(0)
+    _hip.check(_hip.load().lithe_workspace_errors(_hip.ptr(wl.workspace), ctypes.byref(kflags), 1, None),
+               "lithe_workspace_errors")
+    if kflags.value:
+        raise RuntimeError(f"the delta kernels recorded errors during the timed sweeps (flags {kflags.value})")
     tokens = wl.tokens
     value = tokens / (ms * 1e-3)
     per = per_call_times(wl)
@@ -683,6 +691,7 @@ def main():
                      "mean_call_ms": round(call_ms / len(per), 5)},
         "classes": classes,
         "copy_GBps": round(copy_gbps, 1),
+        "kernel_error_flags": kflags.value,
         "cpu_baseline": cpu,
     }
     if wl.decode_ms is not None:
