@@ -1,7 +1,7 @@
 """GPU checks of the delta under the serving patterns the bench uses: HIP-graph replay
-(every replay equal to the eager result, bit for bit), repeated slots (Zipf-style batches
-where several samples share an adapter) and empty routes (-1: the base output stays
-untouched)."""
+(every replay equal to the eager result, bit for bit), calls on two streams at once, repeated
+slots (Zipf-style batches where several samples share an adapter) and empty routes (-1: the
+base output stays untouched)."""
 import ctypes
 
 import numpy as np
@@ -100,3 +100,37 @@ def test_repeated_slots_and_empty_routes():
         assert rel(got[live], want[live]) < 2e-3
         # samples routed to the same slot see the same factors: equal inputs give equal outputs
         assert np.array_equal(got[0], got[1])
+
+
+def test_two_streams_at_once_match_one_stream():
+    """Calls enqueued on two streams at the same time (each stream has its own workspace) give
+    the results of the same calls on one stream, bit for bit, on every repetition."""
+    from lithe_amd.kernels import _hip, packed_lora_delta
+    _, bank = _bank()
+    pools = (bank.pool_a.bfloat16(), bank.pool_b.bfloat16())
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    work = []
+    for name, di, do in MODS:
+        _, _, _, a_off, b_off = bank.layout.module(name)
+        for assign in ([4, 1, 1, 0], [2, 3, 0, 2]):
+            x = torch.randn(4, 200, di, device="cuda", generator=gen).bfloat16()
+            a = torch.tensor(assign, dtype=torch.int32, device="cuda")
+            work.append((x, a, a_off, b_off, do))
+
+    def run(x, a, a_off, b_off, do):
+        return packed_lora_delta(x, bank.words, a_off, b_off, 3, pools, a, 16, do, 0.75)
+
+    want = [run(*w) for w in work]
+    torch.cuda.synchronize()
+    streams = (torch.cuda.Stream(), torch.cuda.Stream())
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for rep in range(3):
+        got = []
+        for i, w in enumerate(work):
+            with torch.cuda.stream(streams[i % 2]):
+                got.append(run(*w))
+        torch.cuda.synchronize()
+        for i, (g, e) in enumerate(zip(got, want)):
+            assert torch.equal(g, e), (rep, i)
+    assert _hip.workspace_errors() == 0
