@@ -71,6 +71,16 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // expand: BO outputs x 64*subs tokens per workgroup.
     int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
     bo_max = std::max(32, bo_max);
+    if (xbytes == 2 && p.GM == 1 && !dense) {
+        // 128-output tiles (76 VGPRs: 6 waves per SIMD with accumulate, against 4) where 256-output
+        // tiles give a mid-sized grid. Measured over the FLUX shapes: grids of 5,376 to 13,824
+        // workgroups 1-3 % faster (the 342-linear sweep 0.45 %), 1,344, 16,128 and 43,008 slower;
+        // dense factors slower (twice the workgroups re-read each B tile)
+        const int64_t wgs256 = n_batch * ((seq + 63) / 64) * ((d_out + 255) / 256);
+        int bo = wgs256 >= 4096 && wgs256 < 14336 ? 128 : 256;
+        if (getenv("LITHE_EXPAND_BO")) bo = env_int("LITHE_EXPAND_BO", bo) == 128 ? 128 : 256;
+        bo_max = bo;
+    }
     p.U = 4;
     p.BOM = bo_max;
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);

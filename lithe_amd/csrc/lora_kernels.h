@@ -1041,7 +1041,10 @@ template <typename XT, typename YT, int SRC>
 void dispatch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
     constexpr bool bf = sizeof(XT) == 2;
     switch (p.GM) {
-        case 1: launch_expand<XT, YT, SRC, 1, bf ? 256 : 128>(p, a, st); break;
+        case 1:
+            if (bf && p.BOM == 256) launch_expand<XT, YT, SRC, 1, 256>(p, a, st);
+            else launch_expand<XT, YT, SRC, 1, 128>(p, a, st);
+            break;
         case 2: launch_expand<XT, YT, SRC, 2, bf ? 256 : 128>(p, a, st); break;
         case 4: launch_expand<XT, YT, SRC, 4, bf ? 128 : 64>(p, a, st); break;
         default: launch_expand<XT, YT, SRC, 8, bf ? 64 : 32>(p, a, st); break;
