@@ -71,15 +71,17 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // expand: BO outputs x 64*subs tokens per workgroup.
     int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
     bo_max = std::max(32, bo_max);
+    bool narrow = false;    // 128-output bf16 tiles of the rule below: one sub-tile
     if (xbytes == 2 && p.GM == 1 && !dense) {
-        // 128-output tiles (76 VGPRs: 6 waves per SIMD with accumulate, against 4) where 256-output
-        // tiles give a mid-sized grid. Measured over the FLUX shapes: grids of 5,376 to 13,824
-        // workgroups 1-3 % faster (the 342-linear sweep 0.45 %), 1,344, 16,128 and 43,008 slower;
-        // dense factors slower (twice the workgroups re-read each B tile)
+        // 128-output tiles (76 VGPRs: 6 waves per SIMD with accumulate, against 4) with one
+        // sub-tile where 256-output tiles give fewer than 14,336 workgroups. Measured over the
+        // FLUX shapes: grids of 1,344 to 13,824 workgroups 1-5 % faster, 16,128 and 43,008
+        // slower; dense factors slower (twice the workgroups re-read each B tile)
         const int64_t wgs256 = n_batch * ((seq + 63) / 64) * ((d_out + 255) / 256);
-        int bo = wgs256 >= 4096 && wgs256 < 14336 ? 128 : 256;
+        int bo = wgs256 < 14336 ? 128 : 256;
         if (getenv("LITHE_EXPAND_BO")) bo = env_int("LITHE_EXPAND_BO", bo) == 128 ? 128 : 256;
         bo_max = bo;
+        narrow = bo == 128;
     }
     p.U = 4;
     p.BOM = bo_max;
@@ -88,7 +90,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
     // 2 sub-tiles of 64 tokens per workgroup only for mid-sized grids (the 512-token, 3072-output
     // FLUX modules); everywhere else one sub-tile (more, shorter workgroups) measured faster.
-    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256) ? 2 : 1;
+    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !narrow) ? 2 : 1;
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
