@@ -290,3 +290,73 @@ def test_per_sample_delta_matches_einsum():
     truth = np.einsum("bsd,brd,bor->bso", odec.round_bf16(x * 0.5), odec.round_bf16(a * 0.02),
                       odec.round_bf16(b * 0.02)) * s[:, None, None]
     assert np.linalg.norm(got16 - truth) / np.linalg.norm(truth) < 1e-2
+
+
+def _lithe_linear_case(scaling):
+    rng = np.random.default_rng(11)
+    d_in, d_out, r = 192, 320, 16
+    ad = random_adapter([("l", d_in, d_out)], rank=r, seed=6)
+    a, b = _factors(ad, "l", d_in, d_out, r)
+    x = odec.round_bf16(rng.standard_normal((3, 40, d_in)).astype(np.float32))
+    base = odec.round_bf16(rng.standard_normal((3, 40, d_out)).astype(np.float32) * 0.01)
+    return x, base, a, b
+
+
+def test_lithe_linear_fp32_closed_form_and_planted_mistakes():
+    """lithe/module.py:154-156 in fp32: base + (x A^T) B^T * scaling, against the float64 closed form.
+    A dropped scaling, a doubled scaling and B read as an (r, d_out) matrix all fail the check."""
+    s = 1.5                                              # alpha / r = 24 / 16
+    x, base, a, b = _lithe_linear_case(s)
+    truth = base.astype(np.float64) + s * odelta.truth_delta(x, a, b)
+    got = odelta.lithe_linear(x, base, a, b, s, "fp32")
+    np.testing.assert_allclose(got, truth, rtol=0, atol=1e-6)
+    r, d_out = a.shape[0], b.shape[0]
+    for wrong in (odelta.lithe_linear(x, base, a, b, 1.0, "fp32"),
+                  odelta.lithe_linear(x, base, a, b, s * s, "fp32"),
+                  odelta.lithe_linear(x, base, a, b.reshape(r, d_out).T.copy(), s, "fp32")):
+        assert np.abs(wrong - truth).max() > 1e-3
+
+
+def test_lithe_linear_bf16_equals_torch_cpu_ops_and_truth_bound():
+    """lithe/module.py:154-156 in bf16, evaluated by torch's own CPU ops (F.linear twice, the
+    bf16 multiply by the scaling, the bf16 add): the oracle's rounding points give the same bits.
+    With a zero base the delta stays within the reference's 2e-2 truth bound
+    (tests/test_kernels.py:216 of the reference). An oracle that kept x A^T unrounded, or
+    skipped the rounding of delta * scaling, would differ in more than a fifth of the outputs."""
+    import torch.nn.functional as F
+    s = 1.5
+    x, base, a, b = _lithe_linear_case(s)
+    tx, ta, tb, tbase = (torch.from_numpy(np.ascontiguousarray(v)).bfloat16() for v in (x, a, b, base))
+    want = (tbase + F.linear(F.linear(tx, ta), tb) * s).float().numpy()
+    got = odelta.lithe_linear(x, base, a, b, s, "bf16")
+    differ = got != want
+    assert differ.mean() < 1e-3                          # torch's fp32 accumulation order may flip a rare tie
+    if differ.any():
+        from helpers import bf16_ulp
+        assert (np.abs(got - want) <= bf16_ulp(want)).all()
+    zero = np.zeros_like(base)
+    d = odelta.lithe_linear(x, zero, a, b, s, "bf16")
+    truth = s * odelta.truth_delta(x, a, b)
+    assert np.linalg.norm(d - truth) / np.linalg.norm(truth) < 2e-2
+    ar, br = odec.round_bf16(a).astype(np.float64), odec.round_bf16(b).astype(np.float64)
+    mid_unrounded = odec.round_bf16(odec.round_bf16((x.astype(np.float64) @ ar.T) @ br.T) * np.float32(s))
+    mid = odec.round_bf16(x.astype(np.float64) @ ar.T).astype(np.float64)
+    scale_unrounded = odec.round_bf16(mid @ br.T) * np.float32(s)
+    for wrong in (odec.round_bf16(base + mid_unrounded), odec.round_bf16(base + scale_unrounded)):
+        assert (wrong != want).mean() > 0.2
+
+
+def test_index_linear_bit_exact_with_torch_add():
+    """lithe/kernels/layers.py:131: ``out + delta`` with both in the activation dtype is torch's
+    bf16 (or fp32) add; the oracle gives the same bits. Leaving the sum unrounded fails."""
+    rng = np.random.default_rng(12)
+    base = odec.round_bf16(rng.standard_normal((4, 33, 96)).astype(np.float32))
+    delta = odec.round_bf16(rng.standard_normal((4, 33, 96)).astype(np.float32) * 0.02)
+    want = (torch.from_numpy(base).bfloat16() + torch.from_numpy(delta).bfloat16()).float().numpy()
+    got = odelta.index_linear(base, delta, "bf16")
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert (base + delta != want).mean() > 0.2
+    b32 = rng.standard_normal((4, 33, 96)).astype(np.float32)
+    d32 = rng.standard_normal((4, 33, 96)).astype(np.float32) * 0.02
+    want32 = (torch.from_numpy(b32) + torch.from_numpy(d32)).numpy()
+    assert np.array_equal(odelta.index_linear(b32, d32, "fp32").view(np.uint32), want32.view(np.uint32))
