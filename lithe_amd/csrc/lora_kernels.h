@@ -578,6 +578,9 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
 // ============================================================================ expand
 template <typename YT>
 __device__ __forceinline__ float finish(float acc, float s, float yold, bool accumulate) {
+    // `delta * scaling` and `out + delta` are two rounded operations in the reference; with fp32 y
+    // nothing rounds between them, so the multiply-add must not be contracted into one fma
+#pragma clang fp contract(off)
     const float d = DT<YT>::round(DT<YT>::round(acc) * s);
     return accumulate ? DT<YT>::round(yold + d) : d;
 }

@@ -1,7 +1,9 @@
 """GPU checks of the delta at the headline workload's real shapes, where the oracle is too slow
 to run whole: B = 14 samples routed to 14 distinct slots of a packed bank, with the shapes of the
-342-linear FLUX sweep (4,608-token single-block q, 4,096-token 3072 -> 12288 up projection,
-512-token 12288 -> 3072 text down projection; the last is planned with K split over 4 waves).
+342-linear FLUX sweep, all seven (d_in, d_out, tokens) classes: 3072 -> 3072 at 4,608 (single-block
+q / k / v), 4,096 (image attention) and 512 (text attention) tokens; 3072 -> 12288 at 4,096 and 512;
+12288 -> 3072 at 4,096 (planned with K split over 2 waves, one rank group) and 512 (K split over 4
+waves).
 
 Size-independent properties, bit-exact (each token's result depends only on its own x row, its
 slot's factors and the plan, which is the same for every sample):
@@ -25,8 +27,10 @@ from oracle import delta as odelta
 from helpers import random_adapter, rel
 
 pytestmark = pytest.mark.gpu
-MODS = [("single.q", 3072, 3072), ("ff.up", 3072, 12288), ("ffc.down", 12288, 3072)]
-TOKENS = {"single.q": 4608, "ff.up": 4096, "ffc.down": 512}
+MODS = [("single.q", 3072, 3072), ("img.q", 3072, 3072), ("txt.q", 3072, 3072), ("ff.up", 3072, 12288),
+        ("ffc.up", 3072, 12288), ("ff.down", 12288, 3072), ("ffc.down", 12288, 3072)]
+TOKENS = {"single.q": 4608, "img.q": 4096, "txt.q": 512, "ff.up": 4096, "ffc.up": 512, "ff.down": 4096,
+          "ffc.down": 512}
 B, RANK, SCALE = 14, 16, 0.75
 
 
