@@ -16,8 +16,9 @@ Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
 the HBM roofline with the algorithmic bytes 2 d_in + 4 d_out per token (x read,
 y read + write) plus the packed index words of the routed adapters;
-``cpu_baseline`` times the oracle (numpy restatement of the reference's
-PyTorch path) on one sample per module class on the host cores.
+``cpu_baseline`` times the reference's serving forward restated in torch CPU ops
+(bf16 bmm, fp32 decode of the routed adapters) over one module per class on the
+host cores; ``env`` records ROCm, torch, the GPU and the host CPU.
 """
 from __future__ import annotations
 
@@ -221,46 +222,93 @@ def copy_bandwidth_gbps():
     return 2 * (1 << 30) / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(mods, batch, budget_s=25.0):
-    """Oracle (numpy restatement of the reference's shared-codebook path) on the host cores.
+def host_threads() -> int:
+    """Host threads the CPU baselines use: the process's CPU affinity, capped by OMP_NUM_THREADS
+    (the box's CPU share) when that is set."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
 
-    Sample: one sample (all its tokens) of one module per (d_in, d_out, tokens) class,
-    extrapolated to the whole sweep by class multiplicity and batch size.
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def environment() -> dict:
+    """ROCm, torch, GPU and host CPU of this run."""
+    import torch
+    rocm = None
+    for p in ("/opt/rocm/.info/version", "/opt/rocm/.info/version-dev"):
+        if os.path.exists(p):
+            with open(p) as fh:
+                rocm = fh.read().strip()
+            break
+    props = torch.cuda.get_device_properties(0)
+    return {"rocm": rocm, "torch": torch.__version__, "torch_hip": torch.version.hip, "gpu": props.name,
+            "gfx": getattr(props, "gcnArchName", None), "cus": props.multi_processor_count,
+            "gpu_mem_GB": round(props.total_memory / 1e9, 1), "cpu_model": cpu_model(),
+            "host_threads": host_threads()}
+
+
+def cpu_baseline(mods, batch, n_slots, budget_s=20.0):
+    """The reference's serving forward restated in torch CPU ops (oracle.torch_cpu: fp32
+    gather-sum decode of the routed adapters every forward, alpha / r folded into B, two bf16
+    torch.bmm, the add into the base output) on the host cores.
+
+    Sample: every sample of one module of each (d_in, d_out, tokens) class with the batch's
+    routing (B distinct adapters of 3 levels of uniformly random indices), timed until about
+    budget_s seconds of work (at least one pass), scaled to the sweep by class multiplicity.
     """
     import numpy as np
+    import torch
 
     from oracle import codebook as ocb
-    from oracle import delta as odelta
-    from oracle import packing as opk
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = len(os.sched_getaffinity(0))
+    from oracle import torch_cpu
+    threads = host_threads()
+    torch.set_num_threads(threads)
     classes = {}
     for _, di, do, m in mods:
         classes[(di, do, m)] = classes.get((di, do, m), 0) + 1
-    pa, pb = ocb.twin_pools()
-    rng = np.random.default_rng(0)
-    total_s, t0 = 0.0, time.perf_counter()
-    timed = 0
-    for (di, do, m), count in sorted(classes.items(), key=lambda kv: kv[0][2]):
-        ia = rng.integers(0, 512, (1, 3, opk.num_blocks((RANK, di))))
-        ib = rng.integers(0, 512, (1, 3, opk.num_blocks((do, RANK))))
-        x = rng.standard_normal((1, m, di)).astype(np.float32)
-        y = rng.standard_normal((1, m, do)).astype(np.float32)
-        t = time.perf_counter()
-        odelta.index_linear(y, odelta.shared_delta(x, ia, pa, ib, pb, [0], RANK, do, 1.0, "bf16"), "bf16")
-        dt = time.perf_counter() - t
-        total_s += dt * count * batch
-        timed += 1
-        if time.perf_counter() - t0 > budget_s:
+    pa, pb = (torch.from_numpy(p) for p in ocb.twin_pools())
+    g = torch.Generator().manual_seed(0)
+    per_class = {}
+    t_start = time.perf_counter()
+    passes = 0
+    while True:
+        for (di, do, m) in sorted(classes):
+            nba, nbb = RANK * di // 64, do * RANK // 64
+            ia = [torch.randint(0, 512, (3, nba), generator=g, dtype=torch.int16) for _ in range(batch)]
+            ib = [torch.randint(0, 512, (3, nbb), generator=g, dtype=torch.int16) for _ in range(batch)]
+            x = torch.randn(batch, m, di, generator=g).bfloat16()
+            y = torch.randn(batch, m, do, generator=g).bfloat16()
+            ids = torch.arange(batch).view(batch, 1)
+            w = torch.ones(batch, 1)
+            scales = torch.ones(batch)
+            t = time.perf_counter()
+            torch_cpu.routed_add(x, y, ids, w, ia, ib, scales, pa, pb, RANK)
+            dt = time.perf_counter() - t
+            per_class[(di, do, m)] = min(per_class.get((di, do, m), dt), dt)
+            del x, y
+        passes += 1
+        if time.perf_counter() - t_start > budget_s:
             break
+    sweep_s = sum(per_class[k] * c for k, c in classes.items())
     tokens = batch * max(m for _, _, _, m in mods)
-    return {"value": tokens / total_s if timed == len(classes) else None, "unit": "tokens/s",
-            "cores": threads, "kind": "port",
-            "sample": f"oracle shared_delta + index_linear, 1 sample x 1 module of each of {len(classes)} "
-                      f"(d_in, d_out, tokens) classes, scaled by class count x batch {batch}"}
+    return {"value": round(tokens / sweep_s, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "sweep_s": round(sweep_s, 3),
+            "sample": f"torch CPU restatement of the reference's serve.py forward (bf16 bmm, per-forward fp32 decode "
+                      f"of the {batch} routed adapters), all {batch} samples of one module of each of {len(classes)} "
+                      f"(d_in, d_out, tokens) classes, best of {passes} pass(es), scaled by class count to the "
+                      f"{len(mods)}-module sweep; {threads} threads"}
 
 
 def cpu_decode_baseline(layout, budget_s=10.0):
@@ -662,7 +710,7 @@ def main():
         with open(tpath) as fh:
             traffic = json.load(fh).get("hbm_bytes_per_launch")
     copy_gbps = copy_bandwidth_gbps()
-    cpu = None if args.no_cpu else cpu_baseline(wl.mods, batch)
+    cpu = None if args.no_cpu else cpu_baseline(wl.mods, batch, n_slots)
     line = {
         "metric": "adapter-delta tokens/s + achieved HBM GB/s (% peak), FLUX linears, B=14 mixed",
         "value": round(value, 1),
@@ -693,6 +741,7 @@ def main():
         "copy_GBps": round(copy_gbps, 1),
         "kernel_error_flags": kflags.value,
         "cpu_baseline": cpu,
+        "env": environment(),
     }
     if wl.decode_ms is not None:
         line["decode_on_swap_ms"] = round(wl.decode_ms, 4)

@@ -360,3 +360,36 @@ def test_index_linear_bit_exact_with_torch_add():
     d32 = rng.standard_normal((4, 33, 96)).astype(np.float32) * 0.02
     want32 = (torch.from_numpy(b32) + torch.from_numpy(d32)).numpy()
     assert np.array_equal(odelta.index_linear(b32, d32, "fp32").view(np.uint32), want32.view(np.uint32))
+
+
+def test_torch_cpu_serving_path_equals_serve_forward():
+    """oracle.torch_cpu (the CPU baseline: the reference's serve.py forward in torch CPU ops) gives
+    the pinned numpy restatement's numbers: fp32 to accumulation-order precision, bf16 to within
+    one bf16 ulp in a small fraction of the outputs (torch's bmm accumulates in fp32)."""
+    from oracle import torch_cpu
+    from helpers import ulp_stats
+    ads = [random_adapter([("fc", 192, 128)], rank=8, seed=s) for s in range(3)]
+    routes = [[(0, 1.0)], [(2, 1.0)], [], [(1, 0.6), (2, 0.4)], [(0, 1.0)]]
+    ids = np.full((5, 2), -1)
+    w = np.zeros((5, 2), np.float32)
+    for i, r in enumerate(routes):
+        for j, (a, wt) in enumerate(r):
+            ids[i, j], w[i, j] = a, wt
+    ia = np.stack([a.indices["fc"]["A"] for a in ads])
+    ib = np.stack([a.indices["fc"]["B"] for a in ads])
+    scales = np.array([2.0, 0.5, 1.5], np.float32)
+    pa, pb = ocb.twin_pools()
+    rng = np.random.default_rng(2)
+    x = odec.round_bf16(rng.standard_normal((5, 12, 192)).astype(np.float32))
+    base = odec.round_bf16(rng.standard_normal((5, 12, 128)).astype(np.float32) * 0.05)
+    args = (torch.from_numpy(ids), torch.from_numpy(w), [torch.from_numpy(v.astype(np.int64)) for v in ia],
+            [torch.from_numpy(v.astype(np.int64)) for v in ib], torch.from_numpy(scales), torch.from_numpy(pa),
+            torch.from_numpy(pb), 8)
+    got32 = torch_cpu.routed_add(torch.from_numpy(x), torch.from_numpy(base), *args).numpy()
+    want32 = odelta.serve_forward(x, base, ids, w, ia, ib, scales, pa, pb, 8, "fp32")
+    np.testing.assert_allclose(got32, want32, rtol=0, atol=1e-6)
+    got16 = torch_cpu.routed_add(torch.from_numpy(x).bfloat16(), torch.from_numpy(base).bfloat16(), *args)
+    want16 = odelta.serve_forward(x, base, ids, w, ia, ib, scales, pa, pb, 8, "bf16")
+    max_ulp, frac = ulp_stats(got16.float().numpy(), want16)
+    assert max_ulp <= 1.0 and frac < 0.02, (max_ulp, frac)
+    assert np.array_equal(got16[2].float().numpy(), base[2])           # the empty route
