@@ -220,6 +220,25 @@ int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_
                          const float *mid_scale, float out_scale, const float *out_scale_vec,
                          void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Bytes of the static scratch lithe_lora_delta_noalloc uses on each GPU (held until the process
+ * ends): the rank-r intermediate of up to 524,288 tokens at rank 16 with bf16 activations. */
+#define LITHE_STATIC_SCRATCH_BYTES 16777216
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): lithe_lora_delta with the
+ * rank-r intermediate in a static device array of LITHE_STATIC_SCRATCH_BYTES per GPU instead of a
+ * workspace. It calls no hipMalloc or hipFree. A call whose intermediate
+ * (lithe_lora_workspace_bytes() - 256 bytes) exceeds the array returns LITHE_ERR_WORKSPACE before any
+ * launch. err_flag (device int32, nullable) receives the in-kernel error bits of lithe_lora_delta's
+ * error word (OR-ed in, never cleared). The array of the current device is shared by every call on
+ * that device and keeps the last call's contents (nothing in it needs to start at zero): calls that
+ * overlap in time on one GPU (other streams, other threads) race and must not be issued. */
+int32_t lithe_lora_delta_noalloc(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
+                                 void *y, int32_t y_dtype, int64_t d_out, int32_t accumulate, int32_t rank,
+                                 const lithe_factors *factors, const lithe_routes *routes,
+                                 const float *mid_scale, float out_scale, const float *out_scale_vec,
+                                 int32_t *err_flag, void *stream);
+
 /* Shared-input group: n_mod modules whose linears read the same x (the to_q / to_k / to_v
  * projections of a FLUX attention block, or add_q / add_k / add_v_proj). One shrink reads x once
  * and produces the rank-r intermediate of every module (mid = x [A_0; A_1; ...]^T, stacked as

@@ -1,7 +1,15 @@
 // Host side of the per-sample LoRA delta: plans, argument checks and the C entry points
-// (lithe_lora_workspace_bytes, lithe_lora_delta, lithe_lora_delta_shared_x,
+// (lithe_lora_workspace_bytes, lithe_lora_delta, lithe_lora_delta_noalloc, lithe_lora_delta_shared_x,
 // lithe_workspace_errors). The kernels are in lora_kernels.h.
+#include <atomic>
+#include <mutex>
+
 #include "lora_kernels.h"
+
+// Static scratch of lithe_lora_delta_noalloc: the rank-r intermediate of one call. Every GPU the
+// library runs on holds its own copy until the process ends. In host code `scratch` only names the
+// symbol; its device address comes from hipGetSymbolAddress (static_scratch() below).
+static __device__ __align__(256) char scratch[LITHE_STATIC_SCRATCH_BYTES];
 
 namespace lithe {
 namespace {
@@ -169,9 +177,11 @@ extern "C" int64_t lithe_lora_workspace_bytes(int64_t n_batch, int64_t seq, int6
 namespace lithe {
 namespace {
 
-// Checks shared by both delta entry points (sizes, dtypes, alignment of x and the workspace).
+// Checks shared by the delta entry points (sizes, dtypes, alignment of x and of the workspace; a call
+// on the static scratch has no workspace to check).
 int32_t check_call(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in, int32_t y_dtype,
-                   int32_t rank, const lithe_routes *routes, int groups_per_module, int n_mod, const void *workspace) {
+                   int32_t rank, const lithe_routes *routes, int groups_per_module, int n_mod, const void *workspace,
+                   bool static_scratch = false) {
     if (!routes) return LITHE_ERR_NULL;
     if (x_dtype != LITHE_DT_BF16 && x_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
     if (y_dtype != LITHE_DT_BF16 && y_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
@@ -181,6 +191,7 @@ int32_t check_call(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq,
     if ((int64_t)groups_per_module * routes->n_route * n_mod > kMaxGroups) return LITHE_ERR_SHAPE;
     if (n_batch == 0 || seq == 0) return LITHE_OK;
     if (!x || !routes->slot) return LITHE_ERR_NULL;
+    if (static_scratch) return ((uintptr_t)x & 15u) ? LITHE_ERR_ALIGN : LITHE_OK;
     if (!workspace) return LITHE_ERR_WORKSPACE;
     if (((uintptr_t)x & 15u) || ((uintptr_t)workspace & 255u)) return LITHE_ERR_ALIGN;
     return LITHE_OK;
@@ -213,12 +224,13 @@ void copy_lut(float dst[kMaxLevels][10], const lithe_lut &l) {
         for (int q = 0; q < 10; ++q) dst[v][q] = l.value[v][q];
 }
 
-// Fields common to the shrink and the expand of a call.
-void set_call_fields(LoraArgs &a, const void *x, char *ws, const Plan &p, int64_t n_batch, int64_t seq, int64_t d_in,
+// Fields common to the shrink and the expand of a call: the error word (nullable) and the base of
+// the rank-r intermediate.
+void set_call_fields(LoraArgs &a, const void *x, int32_t *err, void *mid, int64_t n_batch, int64_t seq, int64_t d_in,
                      int32_t rank, const lithe_routes *routes, const float *mid_scale) {
     a.x = x;
-    a.err = reinterpret_cast<int32_t *>(ws);
-    a.mid = ws + p.off_mid;
+    a.err = err;
+    a.mid = mid;
     a.n_batch = n_batch;
     a.seq = seq;
     a.d_in = d_in;
@@ -245,14 +257,22 @@ void set_module_fields(LoraArgs &a, void *y, int64_t d_out, int32_t accumulate, 
 }  // namespace
 }  // namespace lithe
 
-extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
-                                    void *y, int32_t y_dtype, int64_t d_out, int32_t accumulate, int32_t rank,
-                                    const lithe_factors *f, const lithe_routes *routes, const float *mid_scale,
-                                    float out_scale, const float *out_scale_vec, void *workspace,
-                                    int64_t workspace_bytes, void *stream) {
+namespace lithe {
+namespace {
+
+void *static_scratch();
+
+// Body of lithe_lora_delta and lithe_lora_delta_noalloc. Workspace calls: the error word at
+// `workspace`, the rank-r intermediate 256 bytes further, workspace_bytes in all. Static-scratch
+// calls (workspace NULL, use_static): the intermediate in the current device's static scratch of
+// LITHE_STATIC_SCRATCH_BYTES, the error word at err_flag (nullable).
+int32_t lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in, void *y,
+                   int32_t y_dtype, int64_t d_out, int32_t accumulate, int32_t rank, const lithe_factors *f,
+                   const lithe_routes *routes, const float *mid_scale, float out_scale, const float *out_scale_vec,
+                   void *workspace, int64_t workspace_bytes, bool use_static, int32_t *err_flag, void *stream) {
     if (!f) return LITHE_ERR_NULL;
     const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
-    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, 1, workspace);
+    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, 1, workspace, use_static);
     if (rc || n_batch == 0 || seq == 0) return rc;
     if (d_out < 1) return LITHE_ERR_SHAPE;
     if ((d_out * rank) % kBlock) return LITHE_ERR_ALIGN;
@@ -288,8 +308,17 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     const Plan p = make_plan(n_batch, seq, d_in, d_out, rank, routes->n_route, xbytes, f->kind == LITHE_FACTOR_DENSE,
                              ybytes);
     if (!grids_fit(p, n_batch, d_out, 1)) return LITHE_ERR_SHAPE;
-    if (workspace_bytes < p.total) return LITHE_ERR_WORKSPACE;
-    set_call_fields(a, x, static_cast<char *>(workspace), p, n_batch, seq, d_in, rank, routes, mid_scale);
+    int32_t *err = err_flag;
+    void *mid = nullptr;
+    if (use_static) {
+        if (p.total - p.off_mid > LITHE_STATIC_SCRATCH_BYTES) return LITHE_ERR_WORKSPACE;
+        if (!(mid = static_scratch())) return LITHE_ERR_HIP;
+    } else {
+        if (workspace_bytes < p.total) return LITHE_ERR_WORKSPACE;
+        err = static_cast<int32_t *>(workspace);
+        mid = static_cast<char *>(workspace) + p.off_mid;
+    }
+    set_call_fields(a, x, err, mid, n_batch, seq, d_in, rank, routes, mid_scale);
     set_module_fields(a, y, d_out, accumulate, out_scale, out_scale_vec);
     set_shrink_fields(a, p);
     set_expand_fields(a, p);
@@ -300,6 +329,18 @@ extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_ba
     launch_typed(true, x_dtype, y_dtype, p, a, src, st);
     launch_typed(false, x_dtype, y_dtype, p, a, src, st);
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+}  // namespace
+}  // namespace lithe
+
+extern "C" int32_t lithe_lora_delta(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq, int64_t d_in,
+                                    void *y, int32_t y_dtype, int64_t d_out, int32_t accumulate, int32_t rank,
+                                    const lithe_factors *f, const lithe_routes *routes, const float *mid_scale,
+                                    float out_scale, const float *out_scale_vec, void *workspace,
+                                    int64_t workspace_bytes, void *stream) {
+    return lithe::lora_delta(x, x_dtype, n_batch, seq, d_in, y, y_dtype, d_out, accumulate, rank, f, routes, mid_scale,
+                             out_scale, out_scale_vec, workspace, workspace_bytes, false, nullptr, stream);
 }
 
 extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq,
@@ -344,7 +385,8 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
     const int G1 = n_rg * routes->n_route;
     a.n_slots = f[0].a_idx.n_slots;
     copy_lut(a.luts.v[0], f[0].lut_a);
-    set_call_fields(a, x, static_cast<char *>(workspace), ps, n_batch, seq, d_in, rank, routes, mid_scale);
+    set_call_fields(a, x, static_cast<int32_t *>(workspace), static_cast<char *>(workspace) + ps.off_mid, n_batch, seq,
+                    d_in, rank, routes, mid_scale);
     // Shrink: replicated (one single-module workgroup per tile and module, x shared through the
     // Infinity Cache) unless LITHE_SHARED_X_STACKED asks for the module-stacked kernel (all
     // modules' A rows as rank groups of one workgroup).
@@ -391,4 +433,39 @@ extern "C" int32_t lithe_workspace_errors(const void *workspace, int32_t *flags,
         if (hipStreamSynchronize(st) != hipSuccess) return LITHE_ERR_HIP;
     }
     return LITHE_OK;
+}
+
+namespace lithe {
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void *> g_scratch_addr[kScratchDevices];
+
+// Device address of the current device's static scratch, looked up once per device (with that
+// device current) and kept; nullptr if the lookup fails.
+void *static_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) return nullptr;
+    void *p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
+}  // namespace
+}  // namespace lithe
+
+extern "C" int32_t lithe_lora_delta_noalloc(const void *x, int32_t x_dtype, int64_t n_batch, int64_t seq,
+                                            int64_t d_in, void *y, int32_t y_dtype, int64_t d_out, int32_t accumulate,
+                                            int32_t rank, const lithe_factors *f, const lithe_routes *routes,
+                                            const float *mid_scale, float out_scale, const float *out_scale_vec,
+                                            int32_t *err_flag, void *stream) {
+    return lithe::lora_delta(x, x_dtype, n_batch, seq, d_in, y, y_dtype, d_out, accumulate, rank, f, routes, mid_scale,
+                             out_scale, out_scale_vec, nullptr, 0, true, err_flag, stream);
 }

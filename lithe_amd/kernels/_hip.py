@@ -28,6 +28,7 @@ OK = 0
 ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_RANGE, ERR_WORKSPACE, ERR_HIP, ERR_LEVELS, ERR_UNSUPPORTED = (
     -1, -2, -3, -4, -5, -6, -7, -8, -9)
 DT_BF16, DT_F32, DT_F16, DT_I16, DT_I32, DT_I64, DT_U16 = 1, 2, 3, 4, 5, 6, 7
+STATIC_SCRATCH_BYTES = 16777216
 IDX_PACKED9, IDX_LEVEL_I32, IDX_LEVEL_I16, IDX_BLOCK_I16 = 1, 2, 3, 4
 FACTOR_INDEXED, FACTOR_DENSE = 1, 2
 
@@ -70,6 +71,8 @@ SIGNATURES = {
     "lithe_lora_delta": ([_P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _I32, _I32,
                           ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _F32, _P,
                           _P, _I64, _P], _I32),
+    "lithe_lora_delta_noalloc": ([_P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _I32, _I32,
+                                  ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _F32, _P, _P, _P], _I32),
     "lithe_lora_delta_shared_x": ([_P, _I32, _I64, _I64, _I64, _I32, _P, _I32, _P, _I32, _I32,
                                    ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _P, _P, _I64, _P], _I32),
     "lithe_workspace_errors": ([_P, _P, _I32, _P], _I32),

@@ -290,3 +290,32 @@ def test_launch_grid_limits():
                             _hip.DT_BF16, 256, None, None) == _hip.ERR_SHAPE       # 70,000 selections > 65,535
     assert lib.lithe_unpack9(P, 1 << 45, P, _hip.DT_I64, None) == _hip.ERR_SHAPE
     del words
+
+
+def test_noalloc_delta_argument_errors_before_any_launch():
+    """lithe_lora_delta_noalloc: the checks of lithe_lora_delta, then the static-scratch limit; a call
+    that passes every check on a machine without a GPU fails to find the device (LITHE_ERR_HIP)."""
+    lib = _hip.load()
+    f, words = _indexed(d_in=3072, d_out=3072)
+    slot = np.zeros(14, dtype=np.int32)
+    route = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=None, slot_scale=None, n_route=1)
+
+    def call(fa=f, rt=route, x=1 << 12, n_batch=2, seq=8, rank=16):
+        return lib.lithe_lora_delta_noalloc(ctypes.c_void_p(x), _hip.DT_BF16, n_batch, seq, 3072,
+                                            ctypes.c_void_p(1 << 12), _hip.DT_BF16, 3072, 1, rank,
+                                            ctypes.byref(fa) if fa else None, ctypes.byref(rt) if rt else None, None,
+                                            ctypes.c_float(1.0), None, None, None)
+
+    assert call(fa=None) == _hip.ERR_NULL
+    assert call(rt=None) == _hip.ERR_NULL
+    assert call(x=0) == _hip.ERR_NULL
+    assert call(x=(1 << 12) + 8) == _hip.ERR_ALIGN
+    assert call(n_batch=0) == _hip.OK
+    # 14 x 40,000 tokens x 16 ranks x 2 bytes = 17.9 MB of intermediate > the 16 MiB scratch
+    assert call(n_batch=14, seq=40_000) == _hip.ERR_WORKSPACE
+    assert lib.lithe_lora_workspace_bytes(14, 40_000, 3072, 3072, 16, 1, _hip.DT_BF16) - 256 > _hip.STATIC_SCRATCH_BYTES
+    # 14 x 37,449 tokens fit exactly below the limit: every check passes, then the device lookup
+    assert lib.lithe_lora_workspace_bytes(14, 37_449, 3072, 3072, 16, 1, _hip.DT_BF16) - 256 <= _hip.STATIC_SCRATCH_BYTES
+    if not torch.cuda.is_available():
+        assert call(n_batch=14, seq=37_449) == _hip.ERR_HIP
+    del words
