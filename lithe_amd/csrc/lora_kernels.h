@@ -182,6 +182,16 @@ __device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
     }
 }
 
+// Orders the LDS accesses of one wave around a cross-lane exchange: every access before it (in
+// program order) is complete and visible to the other lanes of the wave before any access after
+// it. The LDS executes one wave's accesses in order, so this costs no wait; it keeps the compiler
+// from moving a lane's accesses across the exchange point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ============================================================================ shrink
 // Workgroup = 4 waves of one sample; each wave owns 16 tokens and 1/ks of every K piece
 // (ks waves share a token group). K is cut into pieces of pb blocks, and the sample's A
@@ -426,11 +436,13 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     };
     // loads [m SL, (m + 1) SL) of a batch (steps of the same range) pass through the stage together
     auto stage_batch = [&](const Batch &bt, int m) __attribute__((always_inline)) {
+        wave_lds_sync();    // the other lanes have read the stage's previous contents
 #pragma unroll
         for (int j = m * SL; j < (m + 1) * SL; ++j) {
             const int t = 8 * (j & 1) + lr;
             *reinterpret_cast<XV *>(stage + (((j - m * SL) >> 1) * 128 + 8 * t + (lc ^ (t >> 1))) * 16) = bt.x[j];
         }
+        wave_lds_sync();    // every lane's chunks are in the stage before any lane reads them
     };
     auto staged = [&](int u, int m) __attribute__((always_inline)) -> XV {
         const int c = 4 * (u & 1) + gq;
@@ -891,6 +903,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
         constexpr int PH = HB / 32;    // MFMA column groups (and y accesses) per exchange
 #pragma unroll
         for (int h = 0; h < BOM / HB; ++h) {
+            wave_lds_sync();    // the other lanes have read the tile's previous contents
 #pragma unroll
             for (int p = h * PH; p < (h + 1) * PH; ++p) {
                 if (p >= np) break;
@@ -901,6 +914,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
                 for (int e = 0; e < 8; ++e) d[e] = (__bf16)(DT<YT>::round(vals[e]) * s_b);
                 *reinterpret_cast<bf16x8 *>(unit(r16, 4 * (p - h * PH) + gq)) = d;
             }
+            wave_lds_sync();    // every lane's deltas are in the tile before any lane reads them
 #pragma unroll
             for (int j = h * PH; j < (h + 1) * PH; ++j) {
                 const int t = 8 * (j & 1) + lr, q = 8 * (j >> 1) + lc;
