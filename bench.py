@@ -55,16 +55,46 @@ def flux_modules(img_tokens: int, txt_tokens: int):
     return mods
 
 
+# Stage of a FLUX target linear inside its block: the linears of one stage of a block are independent
+# of each other (the image and text projections, the two attention outputs, the two up and the two down
+# projections), so a serving step can issue them as one grouped call.
+_STAGES = {"attn.to_q": "proj", "attn.to_k": "proj", "attn.to_v": "proj", "attn.add_q_proj": "proj",
+           "attn.add_k_proj": "proj", "attn.add_v_proj": "proj", "attn.to_out.0": "out", "attn.to_add_out": "out",
+           "ff.net.0.proj": "up", "ff_context.net.0.proj": "up", "ff.net.2": "down", "ff_context.net.2": "down"}
+# linears that read one input: the q / k / v projections of one attention input
+_SHARED_INPUT = {"attn.to_q": "img", "attn.to_k": "img", "attn.to_v": "img", "attn.add_q_proj": "txt",
+                 "attn.add_k_proj": "txt", "attn.add_v_proj": "txt"}
+
+
+def _split(name):
+    """(block prefix, linear suffix) of a FLUX module path."""
+    for suffix in _STAGES:
+        if name.endswith(suffix):
+            return name[: -len(suffix)], suffix
+    raise ValueError(name)
+
+
+def flux_groups(mods):
+    """Indices of ``mods`` grouped by (block, stage), in order of first appearance."""
+    groups = {}
+    for i, (n, _, _, _) in enumerate(mods):
+        prefix, suffix = _split(n)
+        groups.setdefault((prefix, _STAGES[suffix]), []).append(i)
+    return list(groups.values())
+
+
 class Workload:
     """Bank, buffers and prepared per-module calls of one configuration."""
 
-    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0, decoded=False, qkv=False):
+    def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0, decoded=False, qkv=False,
+                 grouped=False):
         import numpy as np
         import torch
 
         from lithe_amd.kernels import PackedBank, PackedLayout
-        from lithe_amd.kernels.prepared import (prepare_dense, prepare_packed, prepare_packed_shared_x,
-                                                shared_workspace, workspace_bytes)
+        from lithe_amd.kernels.prepared import (group_workspace_bytes, prepare_dense, prepare_packed,
+                                                prepare_packed_group, prepare_packed_shared_x, shared_workspace,
+                                                workspace_bytes)
 
         self.name, self.mods, self.batch = name, mods, batch
         dev = torch.device("cuda:0")
@@ -82,7 +112,9 @@ class Workload:
         gen = torch.Generator(device=dev).manual_seed(seed + 1)
         self._bufs, self._next = {}, {}
 
-        def buf(d, m):
+        def buf(d, m, avoid=()):
+            """The next buffer of the (d, m) rotation that is none of ``avoid`` (the buffers of the
+            other modules of the same call); a new copy joins the rotation if all are taken."""
             key = (d, m)
             if key not in self._bufs:
                 nbytes = batch * m * d * 2
@@ -90,11 +122,22 @@ class Workload:
                 self._bufs[key] = [torch.randn(batch, m, d, device=dev, generator=gen).to(torch.bfloat16)
                                    for _ in range(copies)]
                 self._next[key] = 0
-            i = self._next[key]
-            self._next[key] = (i + 1) % len(self._bufs[key])
-            return self._bufs[key][i]
+            pool = self._bufs[key]
+            for _ in range(len(pool)):
+                i = self._next[key]
+                self._next[key] = (i + 1) % len(pool)
+                if all(pool[i] is not t for t in avoid):
+                    return pool[i]
+            pool.append(torch.randn(batch, m, d, device=dev, generator=gen).to(torch.bfloat16))
+            return pool[-1]
 
         need = max(workspace_bytes((batch, m, di), do, RANK, 3 if qkv else 1, torch.bfloat16) for _, di, do, m in mods)
+        groups = flux_groups(mods) if grouped else []
+        for gi in groups:
+            keys = [_SHARED_INPUT.get(_split(mods[i][0])[1], str(i)) if qkv else str(i) for i in gi]
+            ids = {k: j for j, k in enumerate(dict.fromkeys(keys))}
+            need = max(need, group_workspace_bytes([(mods[i][3], mods[i][1], mods[i][2]) for i in gi],
+                                                   [ids[k] for k in keys], batch, RANK, 1, torch.bfloat16))
         self.workspace = shared_workspace(dev, need)
         self.calls = []
         self.call_mods = []
@@ -111,14 +154,32 @@ class Workload:
             self.factors = self.bank.decode_stacked(uniq)
             torch.cuda.synchronize()
             self.decode_ms = (time.perf_counter() - t0) * 1e3
-        k = 0
+        for gi in groups:
+            # one grouped call per (block, stage); with qkv the q / k / v of one input read one x
+            xs, ys, offs, shared = [], [], [], {}
+            for i in gi:
+                n, di, do, m = mods[i]
+                key = _SHARED_INPUT.get(_split(n)[1]) if qkv else None
+                if key is None or key not in shared:
+                    x = buf(di, m, xs + ys)
+                    if key is not None:
+                        shared[key] = x
+                xs.append(shared[key] if key is not None else x)
+                ys.append(buf(do, m, xs + ys))
+                offs.append(layout.module(n)[3:5])
+            self.calls.append(prepare_packed_group(xs, ys, self.bank.words, offs, 3, pools, self.assign, RANK, 1.0,
+                                                   self.workspace, accumulate=True))
+            self.call_mods.append([mods[i] for i in gi])
+        k = len(mods) if grouped else 0
         while k < len(mods):
             n, di, do, m = mods[k]
             if qkv and (n.endswith("attn.to_q") or n.endswith("attn.add_q_proj")):
                 # the three projections of one attention input read the same x
                 group = mods[k:k + 3]
                 x = buf(di, m)
-                ys = [buf(g[2], g[3]) for g in group]
+                ys = []
+                for g in group:
+                    ys.append(buf(g[2], g[3], [x] + ys))
                 offs = [layout.module(g[0])[3:5] for g in group]
                 self.calls.append(prepare_packed_shared_x(x, ys, self.bank.words, offs, 3, pools, self.assign, RANK,
                                                           1.0, self.workspace, accumulate=True))
@@ -128,7 +189,8 @@ class Workload:
             k += 1
             self.call_mods.append([mods[k - 1]])
             _, _, _, a_off, b_off = layout.module(n)
-            x, y = buf(di, m), buf(do, m)
+            x = buf(di, m)
+            y = buf(do, m, [x])
             if decoded:
                 a, b = self.factors[n]
                 self.calls.append(prepare_dense(x, y, a, b, self.sel, RANK, 1.0, self.workspace, accumulate=True))
@@ -619,7 +681,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="flux342",
-                    choices=["flux342", "qkv", "decoded", "ffn", "hb", "decode", "ingest", "encode"])
+                    choices=["flux342", "qkv", "grouped", "fused", "decoded", "ffn", "hb", "decode", "ingest",
+                             "encode"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -648,18 +711,22 @@ def main():
         run_encode(args)
         return
     rng = np.random.default_rng(1234)
-    if args.config in ("flux342", "decoded", "qkv"):
+    if args.config in ("flux342", "decoded", "qkv", "grouped", "fused"):
         mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
         assign = rng.choice(n_slots, batch, replace=False)
         wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config == "decoded",
-                      qkv=args.config == "qkv")
+                      qkv=args.config in ("qkv", "fused"), grouped=args.config in ("grouped", "fused"))
         workload = "FLUX.1-dev 342 linears, 1024^2: B=14 x 4608 tokens (4096 img + 512 txt), 10k-adapter packed bank"
         if args.config == "decoded":
             workload += (", decoded mode: the 14 routed adapters decoded once to stacked bf16 factors "
                          "(decode-on-swap), modules read dense factors")
-        if args.config == "qkv":
-            workload += (", q/k/v fused: the three projections of each attention input read x once "
-                         f"({len(wl.calls)} calls per sweep)")
+        if args.config in ("qkv", "fused"):
+            workload += ", q/k/v fused: the three projections of each attention input read x once"
+        if args.config in ("grouped", "fused"):
+            workload += (", grouped: the independent linears of each block stage (image + text projections, "
+                         "attention outputs, up and down projections) in one shrink + one expand launch")
+        if args.config != "flux342":
+            workload += f" ({len(wl.calls)} calls per sweep)"
     elif args.config == "hb":
         mods, batch, n_slots = flux_modules(256, 512), 96, args.slots or 10_000
         ranks = np.arange(1, n_slots + 1, dtype=np.float64)
@@ -695,7 +762,12 @@ def main():
     classes = {}
     for group, t, c in zip(wl.call_mods, per, wl.calls):
         _, di, do, m = group[0]
-        k = f"{di}->{do} x {m}" if len(group) == 1 else f"{di}->{len(group)}x{do} x {m} (shared x)"
+        if len(group) == 1:
+            k = f"{di}->{do} x {m}"
+        elif args.config in ("grouped", "fused"):
+            k = "group " + " + ".join(sorted({f"{g[1]}->{g[2]} x {g[3]}" for g in group}))
+        else:
+            k = f"{di}->{len(group)}x{do} x {m} (shared x)"
         e = classes.setdefault(k, {"count": 0, "ms": 0.0, "bytes": 0})
         e["count"] += 1
         e["ms"] += t
@@ -730,8 +802,11 @@ def main():
                    "calls_per_step": len(wl.calls)},
         "achieved_GBps": round(wl.alg_bytes / (ms * 1e-3) / 1e9, 1),
         "frac_of_peak": round(wl.alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-        "roofline": {"kernel": "lithe_lora_delta (shrink + expand, one call per module)" if args.config != "qkv"
-                     else "lithe_lora_delta / lithe_lora_delta_shared_x (one shrink + one expand per module)",
+        "roofline": {"kernel": {"qkv": "lithe_lora_delta / lithe_lora_delta_shared_x (one shrink + one expand per module)",
+                                "grouped": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)",
+                                "fused": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage, "
+                                         "q/k/v sharing x)"}.get(args.config,
+                                                                 "lithe_lora_delta (shrink + expand, one call per module)"),
                      "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,

@@ -31,6 +31,7 @@ extern "C" {
 #define LITHE_ERR_HIP       -7   /* a HIP launch or query failed */
 #define LITHE_ERR_LEVELS    -8   /* num_levels outside [1, 4] */
 #define LITHE_ERR_UNSUPPORTED -9 /* weight_sqrt / slot_scale given with dense factors */
+#define LITHE_ERR_OVERLAP  -10   /* two modules of a grouped call write overlapping outputs */
 
 /* ---------------------------------------------------------------- dtype codes */
 #define LITHE_DT_BF16  1
@@ -258,6 +259,42 @@ int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int64_t n_batc
                                   int32_t accumulate, int32_t rank, const lithe_factors *factors,
                                   const lithe_routes *routes, const float *mid_scale, const float *out_scale,
                                   void *workspace, int64_t workspace_bytes, void *stream);
+
+/* One module of a grouped call: its input, its base output and where its factors sit in a slot. */
+typedef struct lithe_module {
+    const void *x;          /* device (n_batch, seq, d_in), 16-byte aligned */
+    void *y;                /* device (n_batch, seq, d_out) */
+    int64_t seq, d_in, d_out;
+    int64_t a_block_off;    /* first block of the module's A (rank x d_in) in a slot of factors->a_idx */
+    int64_t b_block_off;    /* first block of the module's B (d_out x rank) in a slot of factors->b_idx */
+    float out_scale;        /* alpha / r of the module */
+} lithe_module;
+
+#define LITHE_MAX_GROUP_MODULES 8
+
+/* Bytes of workspace lithe_lora_delta_grouped needs for these modules: a 256-byte head (the error
+ * word, as for lithe_lora_workspace_bytes) and the rank-r intermediate of every distinct input. */
+int64_t lithe_lora_grouped_workspace_bytes(int64_t n_batch, int32_t n_mod, const lithe_module *mods, int32_t rank,
+                                           int32_t n_route, int32_t x_dtype);
+
+/* The deltas of n_mod <= LITHE_MAX_GROUP_MODULES independent modules of one batch in one shrink launch
+ * and one expand launch: module m updates mods[m].y exactly as lithe_lora_delta(mods[m].x, ...,
+ * mods[m].y, ..., out_scale = mods[m].out_scale) would (no mid_scale, no out_scale_vec). Modules with
+ * the same x, seq and d_in share one shrink over x (x read once, as lithe_lora_delta_shared_x).
+ * Every module uses the same routes, rank and dtypes, and the same index sources and value tables
+ * (factors: one INDEXED entry whose a_idx / b_idx block_off are ignored: each module's offsets come
+ * from a_block_off / b_block_off). The launch plan is made for the whole grid, so the K split of a
+ * module's shrink can differ from its lithe_lora_delta plan (the fp32 sums are then grouped
+ * differently). Modules with seq == 0 are skipped. Outputs of two modules must not overlap
+ * (LITHE_ERR_OVERLAP); an output may alias another module's input (every shrink ends before the
+ * first expand starts).
+ * Replaces the calls of independent IndexLoRALinear layers of one transformer block that a serving
+ * step issues back to back (the image and text projections of a FLUX double block,
+ * lithe/kernels/layers.py:120-131 via serving/_common.py:294-311), each of which launches its own
+ * shrink and expand (lithe/kernels/shared.py:197-263). */
+int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *mods, int32_t x_dtype, int32_t y_dtype,
+                                 int64_t n_batch, int32_t accumulate, int32_t rank, const lithe_factors *factors,
+                                 const lithe_routes *routes, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Reads the in-kernel error word of a workspace (slot id out of range, index > 511) into
  * *flags on the host; synchronises the stream. 0 = no error since the last clear. */

@@ -21,6 +21,7 @@ extern "C" const char *lithe_status_string(int32_t code) {
         case LITHE_ERR_HIP: return "HIP launch failed";
         case LITHE_ERR_LEVELS: return "num_levels must be in [1, 4] and agree across sources";
         case LITHE_ERR_UNSUPPORTED: return "route weights and slot scales apply to indexed factors only";
+        case LITHE_ERR_OVERLAP: return "two modules of a grouped call write overlapping outputs";
         default: return "unknown status";
     }
 }

@@ -25,8 +25,15 @@ int env_int(const char *name, int dflt) {
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
+// Launch context of a grouped call: the plan rules that depend on the grid's size (the shrink's K
+// split, the expand's tile width and sub-tiles) see the whole grid of the launch, not one job.
+struct PlanCtx {
+    int64_t groups;     // 16-token groups of every shrink job of the launch
+    int64_t wgs256;     // expand workgroups of every job at 256-output tiles
+};
+
 Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int rank, int n_route, int xbytes,
-               bool dense, int ybytes = 2) {
+               bool dense, int ybytes = 2, const PlanCtx *ctx = nullptr) {
     Plan p{};
     p.n_rg = (rank + 15) / 16;
     p.G = p.n_rg * n_route;
@@ -36,7 +43,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     const int target = env_int("LITHE_TARGET_WAVES", 2048);
 
     // shrink: one wave per 16 tokens x (K / ks); ks grows until there are enough waves.
-    const int64_t groups = n_batch * ((seq + 15) / 16);
+    const int64_t groups = ctx ? ctx->groups : n_batch * ((seq + 15) / 16);
     int ks = 1;
     // long K: shorter per-wave streams; with 4 or 8 rank groups a 4-way split costs more in
     // LDS reads than it gains (measured on the q/k/v shared-input shapes)
@@ -85,7 +92,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
         // sub-tile where 256-output tiles give fewer than 14,336 workgroups. Measured over the
         // FLUX shapes: grids of 1,344 to 13,824 workgroups 1-5 % faster, 16,128 and 43,008
         // slower; dense factors slower (twice the workgroups re-read each B tile)
-        const int64_t wgs256 = n_batch * ((seq + 63) / 64) * ((d_out + 255) / 256);
+        const int64_t wgs256 = ctx ? ctx->wgs256 : n_batch * ((seq + 63) / 64) * ((d_out + 255) / 256);
         int bo = wgs256 < 14336 ? 128 : 256;
         if (getenv("LITHE_EXPAND_BO")) bo = env_int("LITHE_EXPAND_BO", bo) == 128 ? 128 : 256;
         bo_max = bo;
@@ -98,7 +105,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
     // 2 sub-tiles of 64 tokens per workgroup only for mid-sized grids (the 512-token, 3072-output
     // FLUX modules); everywhere else one sub-tile (more, shorter workgroups) measured faster.
-    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !narrow) ? 2 : 1;
+    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !narrow && !ctx) ? 2 : 1;
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
@@ -114,6 +121,11 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.off_mid = 256;
     p.total = align256(p.off_mid + rows * p.MR * xbytes);
     return p;
+}
+
+// The grouped kernels are compiled for bf16 activations and outputs with packed 3-level factors.
+bool launch_shrink_group_bf16_ok(int x_dtype, int y_dtype, int src) {
+    return x_dtype == LITHE_DT_BF16 && y_dtype == LITHE_DT_BF16 && src == SRC_PACKED;
 }
 
 int src_of(const LoraArgs &a, int kind) {
@@ -419,6 +431,231 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
         e.mid_goff = m * G1;
         set_expand_fields(e, pe);
         launch_typed(false, x_dtype, y_dtype, pe, e, src_of(e, LITHE_FACTOR_INDEXED), st);
+    }
+    return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+}
+
+namespace lithe {
+namespace {
+
+// Shrink jobs of a grouped call: the modules that read one input (same x, seq and d_in; at most
+// kMaxGroups per job) share a job, each job owns one intermediate region of the workspace.
+struct GroupLayout {
+    int n_sj;
+    int sj_of_mod[kMaxJobs];      // shrink job of module m
+    int pos_in_sj[kMaxJobs];      // module m's place in its job (its rank groups in the job's rows)
+    int n_in_sj[kMaxJobs];        // modules of each job
+    int mods_of_sj[kMaxJobs][kMaxGroups];
+    int64_t mid_off[kMaxJobs];    // byte offset of each job's intermediate
+    int64_t total;                // workspace bytes
+};
+
+void group_layout(int64_t n_batch, int n_mod, const lithe_module *mods, int G, int xbytes, GroupLayout &L) {
+    L = GroupLayout{};
+    for (int m = 0; m < n_mod; ++m) {
+        int j = -1;
+        for (int q = 0; q < L.n_sj && j < 0; ++q) {
+            const lithe_module &f = mods[L.mods_of_sj[q][0]];
+            if (f.x == mods[m].x && f.seq == mods[m].seq && f.d_in == mods[m].d_in && L.n_in_sj[q] < kMaxGroups) j = q;
+        }
+        if (j < 0) j = L.n_sj++;
+        L.sj_of_mod[m] = j;
+        L.pos_in_sj[m] = L.n_in_sj[j];
+        L.mods_of_sj[j][L.n_in_sj[j]++] = m;
+    }
+    int64_t off = 256;
+    for (int q = 0; q < L.n_sj; ++q) {
+        L.mid_off[q] = off;
+        off = align256(off + n_batch * mods[L.mods_of_sj[q][0]].seq * (int64_t)L.n_in_sj[q] * G * 16 * xbytes);
+    }
+    L.total = off;
+}
+
+int64_t round8(int64_t v) { return (v + 7) / 8 * 8; }
+
+}  // namespace
+}  // namespace lithe
+
+extern "C" int64_t lithe_lora_grouped_workspace_bytes(int64_t n_batch, int32_t n_mod, const lithe_module *mods,
+                                                      int32_t rank, int32_t n_route, int32_t x_dtype) {
+    if (!mods) return LITHE_ERR_NULL;
+    if (n_mod < 1 || n_mod > kMaxJobs || n_batch < 0 || rank < 1 || n_route < 1) return LITHE_ERR_SHAPE;
+    if (x_dtype != LITHE_DT_BF16 && x_dtype != LITHE_DT_F32) return LITHE_ERR_DTYPE;
+    const int G = ((rank + 15) / 16) * n_route;
+    if (G > kMaxGroups) return LITHE_ERR_SHAPE;
+    for (int m = 0; m < n_mod; ++m)
+        if (mods[m].seq < 0) return LITHE_ERR_SHAPE;
+    GroupLayout L;
+    group_layout(n_batch, n_mod, mods, G, x_dtype == LITHE_DT_BF16 ? 2 : 4, L);
+    return L.total;
+}
+
+extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *mods_in, int32_t x_dtype,
+                                            int32_t y_dtype, int64_t n_batch, int32_t accumulate, int32_t rank,
+                                            const lithe_factors *f, const lithe_routes *routes, void *workspace,
+                                            int64_t workspace_bytes, void *stream) {
+    if (!mods_in || !f) return LITHE_ERR_NULL;
+    if (n_mod < 1 || n_mod > kMaxJobs) return LITHE_ERR_SHAPE;
+    if (f->kind != LITHE_FACTOR_INDEXED) return LITHE_ERR_UNSUPPORTED;
+    const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
+    const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
+    const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
+    // validate every module as lithe_lora_delta would; keep those with tokens
+    lithe_module mods[kMaxJobs];
+    int n_act = 0;
+    for (int m = 0; m < n_mod; ++m) {
+        const lithe_module &md = mods_in[m];
+        int32_t rc = check_call(md.x, x_dtype, n_batch, md.seq, md.d_in, y_dtype, rank, routes, n_rg, 1, workspace);
+        if (rc) return rc;
+        if (n_batch == 0 || md.seq == 0) continue;
+        if (md.d_out < 1) return LITHE_ERR_SHAPE;
+        if ((md.d_out * rank) % kBlock) return LITHE_ERR_ALIGN;
+        if (!md.y) return LITHE_ERR_NULL;
+        if ((uintptr_t)md.y & (uintptr_t)(ybytes - 1)) return LITHE_ERR_ALIGN;
+        lithe_factors fm = *f;
+        fm.a_idx.block_off = md.a_block_off;
+        fm.b_idx.block_off = md.b_block_off;
+        rc = check_indexed(&fm, rank, md.d_in, md.d_out);
+        if (rc) return rc;
+        mods[n_act++] = md;
+    }
+    if (n_act == 0) return LITHE_OK;
+    for (int m = 0; m < n_act; ++m)
+        for (int q = m + 1; q < n_act; ++q) {
+            const uintptr_t lo0 = (uintptr_t)mods[m].y, lo1 = (uintptr_t)mods[q].y;
+            const uintptr_t hi0 = lo0 + (uintptr_t)(n_batch * mods[m].seq * mods[m].d_out * ybytes);
+            const uintptr_t hi1 = lo1 + (uintptr_t)(n_batch * mods[q].seq * mods[q].d_out * ybytes);
+            if (lo0 < hi1 && lo1 < hi0) return LITHE_ERR_OVERLAP;
+        }
+    const int G = n_rg * routes->n_route;
+    GroupLayout L;
+    group_layout(n_batch, n_act, mods, G, xbytes, L);
+    if (workspace_bytes < L.total) return LITHE_ERR_WORKSPACE;
+
+    PlanCtx ctx{0, 0};
+    for (int q = 0; q < L.n_sj; ++q) ctx.groups += n_batch * ((mods[L.mods_of_sj[q][0]].seq + 15) / 16);
+    for (int m = 0; m < n_act; ++m) ctx.wgs256 += n_batch * ((mods[m].seq + 63) / 64) * ((mods[m].d_out + 255) / 256);
+
+    // common fields; each job's fields are applied over them
+    char *ws = static_cast<char *>(workspace);
+    LoraArgs a{};
+    a.a_src = make_src(f->a_idx);
+    a.a_src.block_off = 0;
+    a.b_src = make_src(f->b_idx);
+    a.n_slots = std::min(f->a_idx.n_slots, f->b_idx.n_slots);
+    copy_lut(a.luts.v[0], f->lut_a);
+    copy_lut(a.luts.v[1], f->lut_b);
+    set_call_fields(a, mods[0].x, reinterpret_cast<int32_t *>(ws), ws + L.mid_off[0], n_batch, mods[0].seq,
+                    mods[0].d_in, rank, routes, nullptr);
+    set_module_fields(a, mods[0].y, mods[0].d_out, accumulate, 1.0f, nullptr);
+    a.G1 = G;
+    const int src = src_of(a, LITHE_FACTOR_INDEXED);
+
+    // shrink jobs, largest first (the short ones fill the tail of the grid)
+    GroupArgs gs{};
+    gs.a = a;
+    Plan ps[kMaxJobs];
+    int order[kMaxJobs];
+    for (int q = 0; q < L.n_sj; ++q) order[q] = q;
+    auto sj_work = [&](int q) { const lithe_module &md = mods[L.mods_of_sj[q][0]]; return md.seq * md.d_in * L.n_in_sj[q]; };
+    std::stable_sort(order, order + L.n_sj, [&](int u, int v) { return sj_work(u) > sj_work(v); });
+    int64_t wg = 0;
+    size_t lds_s = 0;
+    for (int k = 0; k < L.n_sj; ++k) {
+        const int q = order[k];
+        const lithe_module &md = mods[L.mods_of_sj[q][0]];
+        const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route, xbytes, false, ybytes, &ctx);
+        ps[k] = p;
+        set_shrink_fields(gs.a, p);       // G, n_rg (the same for every job)
+        GroupJob &j = gs.job[k];
+        j.x = md.x;
+        j.y = md.y;
+        j.mid = ws + L.mid_off[q];
+        j.seq = md.seq;
+        j.d_in = md.d_in;
+        j.d_out = md.d_out;
+        j.rows = n_batch * md.seq;
+        const int nm = L.n_in_sj[q];
+        for (int g = 0; g < kMaxGroups; ++g) j.a_goff[g] = mods[L.mods_of_sj[q][std::min(g, nm - 1)]].a_block_off;
+        j.MR = nm * G * 16;
+        j.n_mod_wg = nm;
+        j.xnt = nm > 1 ? 0 : 1;
+        j.tiles_s = p.tiles_s;
+        j.ks = p.ks;
+        j.pb = p.pb;
+        j.arow = p.arow;
+        j.region = p.region;
+        j.red_off = p.red_off;
+        j.stage_off = p.stage_off;
+        gs.begin[k] = (int32_t)wg;
+        const int64_t tiles = n_batch * p.tiles_s;
+        wg += round8(nm > 1 ? round8(tiles) * nm : tiles);
+        lds_s = std::max(lds_s, p.lds_s);
+    }
+    gs.n_jobs = L.n_sj;
+    const int64_t grid_s = wg;
+
+    // expand jobs (one per module), largest first
+    GroupArgs ge{};
+    ge.a = a;
+    Plan pe[kMaxJobs];
+    for (int m = 0; m < n_act; ++m) order[m] = m;
+    std::stable_sort(order, order + n_act,
+                     [&](int u, int v) { return mods[u].seq * mods[u].d_out > mods[v].seq * mods[v].d_out; });
+    wg = 0;
+    size_t lds_e = 0;
+    for (int k = 0; k < n_act; ++k) {
+        const int m = order[k];
+        const lithe_module &md = mods[m];
+        const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route, xbytes, false, ybytes, &ctx);
+        pe[k] = p;
+        set_shrink_fields(ge.a, p);
+        GroupJob &j = ge.job[k];
+        const int q = L.sj_of_mod[m];
+        j.x = md.x;
+        j.y = md.y;
+        j.mid = ws + L.mid_off[q];
+        j.seq = md.seq;
+        j.d_in = md.d_in;
+        j.d_out = md.d_out;
+        j.rows = n_batch * md.seq;
+        for (int g = 0; g < kMaxGroups; ++g) j.a_goff[g] = md.a_block_off;
+        j.b_off = md.b_block_off;
+        j.MR = L.n_in_sj[q] * G * 16;
+        j.mid_goff = L.pos_in_sj[m] * G;
+        j.n_mod_wg = 1;
+        j.tiles_e = p.tiles_e;
+        j.subs_e = p.subs_e;
+        j.BO = p.BO;
+        j.vec_y = (md.d_out % 8 == 0) && (((uintptr_t)md.y & 15u) == 0);
+        j.nblk_max = p.nblk_max;
+        j.estage_off = p.estage_off;
+        j.out_scale = md.out_scale;
+        ge.begin[k] = (int32_t)wg;
+        wg += round8(((md.d_out + p.BO - 1) / p.BO) * n_batch * p.tiles_e);
+        lds_e = std::max(lds_e, p.lds_e);
+    }
+    ge.n_jobs = n_act;
+    const int64_t grid_e = wg;
+    if (grid_s > kMaxGridX || grid_e > kMaxGridX) return LITHE_ERR_SHAPE;
+
+    hipStream_t st = (hipStream_t)stream;
+    const bool grouped = getenv("LITHE_GROUPED_SERIAL") == nullptr;
+    if (grouped && launch_shrink_group_bf16_ok(x_dtype, y_dtype, src)) {
+        launch_shrink_group_bf16(ps[0].GM, gs, (unsigned)grid_s, lds_s, src, st);
+        launch_expand_group_bf16_bf16(pe[0].GM, pe[0].BOM, ge, (unsigned)grid_e, lds_e, src, st);
+    } else {
+        // job by job through the per-call kernels (other dtypes and factor kinds)
+        for (int k = 0; k < gs.n_jobs; ++k) {
+            LoraArgs aj = gs.a;
+            apply_job(aj, gs.job[k]);
+            launch_typed(true, x_dtype, y_dtype, ps[k], aj, src, st);
+        }
+        for (int k = 0; k < ge.n_jobs; ++k) {
+            LoraArgs aj = ge.a;
+            apply_job(aj, ge.job[k]);
+            launch_typed(false, x_dtype, y_dtype, pe[k], aj, src, st);
+        }
     }
     return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
 }

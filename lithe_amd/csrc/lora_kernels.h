@@ -118,6 +118,30 @@ struct Plan {
     int64_t off_mid, total;
 };
 
+// Grouped launch: one shrink grid (or one expand grid) over several jobs of one call. Workgroups
+// [begin[j], begin[j + 1]) run job j; a job's fields replace those of the common LoraArgs.
+// Shrink job: one x (one module, or the modules of a shared input in replicated form). Expand job:
+// one module. Every job shares the routes, rank, dtypes and the index sources' bases and tables.
+constexpr int kMaxJobs = 8;
+struct GroupJob {
+    const void *x;
+    void *y;
+    void *mid;
+    int64_t seq, d_in, d_out, rows;
+    int64_t a_goff[kMaxGroups];
+    int64_t b_off;
+    int32_t MR, mid_goff, n_mod_wg, xnt;
+    int32_t tiles_s, ks, pb, arow, region, red_off, stage_off;
+    int32_t tiles_e, subs_e, BO, vec_y, nblk_max, estage_off;
+    float out_scale;
+};
+struct GroupArgs {
+    LoraArgs a;                 // common fields
+    GroupJob job[kMaxJobs];
+    int32_t begin[kMaxJobs];    // first workgroup of each job (multiples of 8: XCD rounds stay aligned)
+    int32_t n_jobs;
+};
+
 namespace {
 
 // Slot of route entry j of sample b, or -1 (empty entry or out of range; the latter is recorded).
@@ -203,8 +227,10 @@ __device__ __forceinline__ void wave_lds_sync() {
 // through LDS in a fixed order (deterministic).
 // XNT: x loads carry the non-temporal hint (x is read once). The replicated shared-input form
 // reads each x line from several workgroups of one XCD and keeps it in L2 instead.
+// bid: the workgroup's index within this call's grid (a grouped launch passes it relative to the
+// call's first workgroup); ids past the call's tiles (padding) return at once.
 template <typename XT, int SRC, int GM, int U, bool XNT>
-__global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
+__device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     constexpr bool kBf16 = sizeof(XT) == 2;
     constexpr int KSTEP = kBf16 ? 32 : 16;
@@ -221,13 +247,13 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     // Replicated mode: workgroups are dealt round-robin to the 8 XCDs, so id w runs on XCD w % 8.
     // The modules of tile t sit at ids 8 (M (t / 8) + m) + t % 8: one XCD, consecutive in its
     // queue, sharing that XCD's L2 for x.
-    int mod = 0, tile = (int)blockIdx.x;
+    int mod = 0, tile = bid;
     if (a.n_mod_wg > 1) {
-        const int q = (int)(blockIdx.x >> 3);
+        const int q = bid >> 3;
         mod = q % a.n_mod_wg;
-        tile = (q / a.n_mod_wg) * 8 + (int)(blockIdx.x & 7);
-        if (tile >= (int)a.n_batch * a.tiles_s) return;    // padding of the last XCD round (before any barrier)
+        tile = (q / a.n_mod_wg) * 8 + (bid & 7);
     }
+    if (tile >= (int)a.n_batch * a.tiles_s) return;    // padding (an XCD round, a grouped call): before any barrier
     const int64_t b = tile / a.tiles_s;
     const int mt = tile % a.tiles_s;
     const int64_t m = ((int64_t)mt * tgw + tgi) * 16 + r16;
@@ -587,6 +613,11 @@ __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
     }
 }
 
+template <typename XT, int SRC, int GM, int U, bool XNT>
+__global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
+    shrink_body<XT, SRC, GM, U, XNT>(a, (int)blockIdx.x);
+}
+
 // ============================================================================ expand
 template <typename YT>
 __device__ __forceinline__ float finish(float acc, float s, float yold, bool accumulate) {
@@ -624,7 +655,7 @@ template <> struct Y8<float> {
 };
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
-__device__ __forceinline__ void expand_body(const LoraArgs &a) {
+__device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     // bf16 y with output tiles of whole lines: the whole-line y path (line_subtile below)
     constexpr bool LINE = sizeof(YT) == 2 && BOM % 64 == 0;
@@ -633,8 +664,9 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
     const int o_tiles = (int)((a.d_out + a.BO - 1) / a.BO);
-    const int64_t obase = (int64_t)(blockIdx.x % o_tiles) * a.BO;
-    const int tile = blockIdx.x / o_tiles;
+    const int64_t obase = (int64_t)(bid % o_tiles) * a.BO;
+    const int tile = bid / o_tiles;
+    if (tile >= (int)a.n_batch * a.tiles_e) return;    // padding of a grouped call (before any barrier)
     const int64_t b = tile / a.tiles_e;
     const int mt = tile % a.tiles_e;
     const float s_b = a.out_scale_vec ? a.out_scale_vec[b] : a.out_scale;
@@ -994,11 +1026,11 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a) {
 // bf16 output).
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
 __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a);
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a, (int)blockIdx.x);
 }
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) expand_kernel_w4(LoraArgs a) {
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a);
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a, (int)blockIdx.x);
 }
 
 #ifndef LITHE_SHARED_X_NT
@@ -1043,6 +1075,124 @@ void launch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
     }
 }
 
+// Job of workgroup `bid` of a grouped launch (scalar compares over the job table).
+__device__ __forceinline__ int group_job(const GroupArgs &g, int bid) {
+    int j = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxJobs; ++q) j += (q < g.n_jobs && bid >= g.begin[q]) ? 1 : 0;
+    return j;
+}
+
+__host__ __device__ __forceinline__ void apply_job(LoraArgs &a, const GroupJob &j) {
+    a.x = j.x;
+    a.y = j.y;
+    a.mid = j.mid;
+    a.seq = j.seq;
+    a.d_in = j.d_in;
+    a.d_out = j.d_out;
+    a.rows = j.rows;
+#pragma unroll
+    for (int q = 0; q < kMaxGroups; ++q) a.a_goff[q] = j.a_goff[q];
+    a.b_src.block_off = j.b_off;
+    a.MR = j.MR;
+    a.mid_goff = j.mid_goff;
+    a.n_mod_wg = j.n_mod_wg;
+    a.tiles_s = j.tiles_s;
+    a.ks = j.ks;
+    a.pb = j.pb;
+    a.arow = j.arow;
+    a.region = j.region;
+    a.red_off = j.red_off;
+    a.stage_off = j.stage_off;
+    a.tiles_e = j.tiles_e;
+    a.subs_e = j.subs_e;
+    a.BO = j.BO;
+    a.vec_y = j.vec_y;
+    a.nblk_max = j.nblk_max;
+    a.estage_off = j.estage_off;
+    a.out_scale = j.out_scale;
+}
+
+// The x loads of a job take the non-temporal hint unless the job is a replicated shared input
+// (its modules' workgroups read each x line from L2); the choice is uniform per workgroup.
+template <typename XT, int SRC, int GM, int U>
+__global__ void __launch_bounds__(kThreads) shrink_group_kernel(GroupArgs g) {
+    const int bid = (int)blockIdx.x;
+    const int j = group_job(g, bid);
+    LoraArgs a = g.a;
+    apply_job(a, g.job[j]);
+    if (g.job[j].xnt) shrink_body<XT, SRC, GM, U, true>(a, bid - g.begin[j]);
+    else shrink_body<XT, SRC, GM, U, false>(a, bid - g.begin[j]);
+}
+
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+__device__ __forceinline__ void expand_group_body(const GroupArgs &g) {
+    const int bid = (int)blockIdx.x;
+    const int j = group_job(g, bid);
+    LoraArgs a = g.a;
+    apply_job(a, g.job[j]);
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a, bid - g.begin[j]);
+}
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+__global__ void __launch_bounds__(kThreads) expand_group_kernel(GroupArgs g) {
+    expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(g);
+}
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) expand_group_kernel_w4(GroupArgs g) {
+    expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(g);
+}
+
+template <typename XT, int SRC, int GM>
+void launch_shrink_group(const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((shrink_group_kernel<XT, SRC, GM, kShrinkU>), dim3(grid), dim3(kThreads), lds, st, g);
+}
+
+template <typename XT, typename YT, int SRC, int GM, int BOM>
+void launch_expand_group(const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+    const bool quad = (g.a.rank & 3) == 0;
+    const dim3 ge(grid);
+    if constexpr (GM == 1 && sizeof(YT) == 2) {
+        if (quad) {
+            if (g.a.accumulate)
+                hipLaunchKernelGGL((expand_group_kernel_w4<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), lds, st, g);
+            else
+                hipLaunchKernelGGL((expand_group_kernel_w4<XT, YT, SRC, GM, BOM, false, true>), ge, dim3(kThreads), lds, st, g);
+            return;
+        }
+    }
+    if (g.a.accumulate) {
+        if (quad) hipLaunchKernelGGL((expand_group_kernel<XT, YT, SRC, GM, BOM, true, true>), ge, dim3(kThreads), lds, st, g);
+        else hipLaunchKernelGGL((expand_group_kernel<XT, YT, SRC, GM, BOM, true, false>), ge, dim3(kThreads), lds, st, g);
+    } else {
+        if (quad) hipLaunchKernelGGL((expand_group_kernel<XT, YT, SRC, GM, BOM, false, true>), ge, dim3(kThreads), lds, st, g);
+        else hipLaunchKernelGGL((expand_group_kernel<XT, YT, SRC, GM, BOM, false, false>), ge, dim3(kThreads), lds, st, g);
+    }
+}
+
+template <typename XT, int SRC>
+void dispatch_shrink_group(int GM, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+    switch (GM) {
+        case 1: launch_shrink_group<XT, SRC, 1>(g, grid, lds, st); break;
+        case 2: launch_shrink_group<XT, SRC, 2>(g, grid, lds, st); break;
+        case 4: launch_shrink_group<XT, SRC, 4>(g, grid, lds, st); break;
+        default: launch_shrink_group<XT, SRC, 8>(g, grid, lds, st); break;
+    }
+}
+
+// BOM as in dispatch_expand (bf16 activations).
+template <typename XT, typename YT, int SRC>
+void dispatch_expand_group(int GM, int BOM, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+    switch (GM) {
+        case 1:
+            if (BOM == 256) launch_expand_group<XT, YT, SRC, 1, 256>(g, grid, lds, st);
+            else launch_expand_group<XT, YT, SRC, 1, 128>(g, grid, lds, st);
+            break;
+        case 2: launch_expand_group<XT, YT, SRC, 2, 256>(g, grid, lds, st); break;
+        case 4: launch_expand_group<XT, YT, SRC, 4, 128>(g, grid, lds, st); break;
+        default: launch_expand_group<XT, YT, SRC, 8, 64>(g, grid, lds, st); break;
+    }
+}
+
 template <typename XT, int SRC>
 void dispatch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
     switch (p.GM) {
@@ -1078,5 +1228,10 @@ void launch_expand_bf16_bf16(const Plan &p, const LoraArgs &a, int src, hipStrea
 void launch_expand_bf16_f32(const Plan &p, const LoraArgs &a, int src, hipStream_t st);
 void launch_expand_f32_bf16(const Plan &p, const LoraArgs &a, int src, hipStream_t st);
 void launch_expand_f32_f32(const Plan &p, const LoraArgs &a, int src, hipStream_t st);
+// Grouped launches (bf16 activations and outputs, packed 3-level factors); false if the call has
+// no grouped kernel (the caller then launches job by job).
+bool launch_shrink_group_bf16(int GM, const GroupArgs &g, unsigned grid, size_t lds, int src, hipStream_t st);
+bool launch_expand_group_bf16_bf16(int GM, int BOM, const GroupArgs &g, unsigned grid, size_t lds, int src,
+                                   hipStream_t st);
 
 }  // namespace lithe

@@ -27,6 +27,7 @@ LIB_PATH = os.path.join(_PKG, "_lib", "liblithe_amd.so")
 OK = 0
 ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_DTYPE, ERR_RANGE, ERR_WORKSPACE, ERR_HIP, ERR_LEVELS, ERR_UNSUPPORTED = (
     -1, -2, -3, -4, -5, -6, -7, -8, -9)
+ERR_OVERLAP = -10
 DT_BF16, DT_F32, DT_F16, DT_I16, DT_I32, DT_I64, DT_U16 = 1, 2, 3, 4, 5, 6, 7
 STATIC_SCRATCH_BYTES = 16777216
 IDX_PACKED9, IDX_LEVEL_I32, IDX_LEVEL_I16, IDX_BLOCK_I16 = 1, 2, 3, 4
@@ -57,6 +58,15 @@ class Routes(ctypes.Structure):
                 ("slot_scale", ctypes.c_void_p), ("n_route", ctypes.c_int32)]
 
 
+class Module(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("seq", ctypes.c_int64), ("d_in", ctypes.c_int64),
+                ("d_out", ctypes.c_int64), ("a_block_off", ctypes.c_int64), ("b_block_off", ctypes.c_int64),
+                ("out_scale", ctypes.c_float)]
+
+
+MAX_GROUP_MODULES = 8
+
+
 # Every symbol include/lithe_amd.h declares, with its ctypes signature.
 _P, _I32, _I64, _F32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
@@ -76,6 +86,9 @@ SIGNATURES = {
     "lithe_lora_delta_shared_x": ([_P, _I32, _I64, _I64, _I64, _I32, _P, _I32, _P, _I32, _I32,
                                    ctypes.POINTER(Factors), ctypes.POINTER(Routes), _P, _P, _P, _I64, _P], _I32),
     "lithe_workspace_errors": ([_P, _P, _I32, _P], _I32),
+    "lithe_lora_grouped_workspace_bytes": ([_I64, _I32, _P, _I32, _I32, _I32], _I64),
+    "lithe_lora_delta_grouped": ([_I32, _P, _I32, _I32, _I64, _I32, _I32, ctypes.POINTER(Factors),
+                                  ctypes.POINTER(Routes), _P, _I64, _P], _I32),
     "lithe_decode_stacked": ([ctypes.POINTER(IndexSrc), _P, _I32, _I64, _I32, _P, _P, ctypes.POINTER(Lut),
                               ctypes.POINTER(Lut), _P, _I32, _P, _P], _I32),
     "lithe_encode": ([_P, _I64, _P, ctypes.POINTER(Lut), ctypes.POINTER(Lut), _P, _I32, _I64, _I64, _P, _P], _I32),

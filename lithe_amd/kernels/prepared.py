@@ -151,3 +151,85 @@ def prepare_packed_shared_x(x: torch.Tensor, ys: Sequence[torch.Tensor], bank_wo
     sl = slots.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
     return PreparedSharedX(x, ys, fs, _delta.routes(sl), rank, [scaling] * len(ys), workspace, accumulate,
                            keep=(sl, bank_words))
+
+
+def group_workspace_bytes(shapes: Sequence[Tuple[int, int, int]], shared: Sequence[int], n_batch: int, rank: int,
+                          n_route: int, x_dtype: torch.dtype) -> int:
+    """Workspace of a grouped call: ``shapes`` [(seq, d_in, d_out)] per module; modules with equal
+    ``shared`` keys read one input (``lithe_lora_grouped_workspace_bytes``)."""
+    mods = (_hip.Module * len(shapes))()
+    for i, ((seq, d_in, d_out), key) in enumerate(zip(shapes, shared)):
+        mods[i].x = 16 * (key + 1)          # stands for the input's identity only
+        mods[i].seq, mods[i].d_in, mods[i].d_out = seq, d_in, d_out
+    n = _hip.load().lithe_lora_grouped_workspace_bytes(n_batch, len(shapes), mods, rank, n_route,
+                                                       _hip.dtype_code(x_dtype))
+    _hip.check(int(n) if n < 0 else 0, "lithe_lora_grouped_workspace_bytes")
+    return int(n)
+
+
+class PreparedGroup:
+    """y_m <- y_m + delta_m(x_m) for up to 8 independent modules of one batch in one shrink and one
+    expand launch (``lithe_lora_delta_grouped``); modules given the same x tensor share its shrink."""
+
+    def __init__(self, xs: Sequence[torch.Tensor], ys: Sequence[torch.Tensor], factors: _hip.Factors,
+                 offsets: Sequence[Tuple[int, int]], route: _hip.Routes, rank: int, out_scales: Sequence[float],
+                 workspace: torch.Tensor, accumulate: bool = True, keep: Sequence = ()):
+        n = len(xs)
+        if not (n == len(ys) == len(offsets) == len(out_scales)) or not 1 <= n <= _hip.MAX_GROUP_MODULES:
+            raise ValueError(f"a group holds 1 to {_hip.MAX_GROUP_MODULES} modules, each with x, y, offsets and a scale")
+        _hip.require_gpu(workspace, *xs, *ys)
+        b = xs[0].shape[0]
+        for x, y in zip(xs, ys):
+            if x.dim() != 3 or y.dim() != 3 or not x.is_contiguous() or not y.is_contiguous():
+                raise ValueError("every x and y must be a contiguous (B, M, D) tensor")
+            if x.shape[0] != b or y.shape[:2] != x.shape[:2] or x.dtype != xs[0].dtype or y.dtype != ys[0].dtype:
+                raise ValueError("every module needs y (B, M, d_out) over its x (B, M, d_in), one batch and dtype")
+        self.xs, self.ys, self.workspace = list(xs), list(ys), workspace
+        self._m = (_hip.Module * n)()
+        for i, (x, y, (ao, bo), s) in enumerate(zip(xs, ys, offsets, out_scales)):
+            self._m[i].x, self._m[i].y = x.data_ptr(), y.data_ptr()
+            self._m[i].seq, self._m[i].d_in, self._m[i].d_out = x.shape[1], x.shape[2], y.shape[2]
+            self._m[i].a_block_off, self._m[i].b_block_off = int(ao), int(bo)
+            self._m[i].out_scale = float(s)
+        self._lib = _hip.load()
+        need = self._lib.lithe_lora_grouped_workspace_bytes(b, n, self._m, rank, route.n_route,
+                                                            _hip.dtype_code(xs[0].dtype))
+        _hip.check(int(need) if need < 0 else 0, "lithe_lora_grouped_workspace_bytes")
+        if workspace.numel() < need:
+            raise ValueError(f"workspace holds {workspace.numel()} bytes, the call needs {need}")
+        self._f = factors
+        self._keep: List = [route, *keep]
+        self._args = (n, self._m, _hip.dtype_code(xs[0].dtype), _hip.dtype_code(ys[0].dtype), b,
+                      int(bool(accumulate)), int(rank), ctypes.byref(factors), ctypes.byref(route),
+                      _hip.ptr(workspace), workspace.numel())
+        self.tokens = b * max(x.shape[1] for x in xs)
+
+    def algorithmic_bytes(self) -> int:
+        """Every distinct x read once + every y read and written."""
+        seen, total = set(), 0
+        for x in self.xs:
+            if x.data_ptr() not in seen:
+                seen.add(x.data_ptr())
+                total += x.numel() * x.element_size()
+        return total + sum(2 * y.numel() * y.element_size() for y in self.ys)
+
+    def __call__(self, stream: Optional[ctypes.c_void_p] = None) -> None:
+        rc = self._lib.lithe_lora_delta_grouped(*self._args,
+                                                stream if stream is not None else _hip.stream_of(self.xs[0].device))
+        if rc:
+            _hip.check(rc, "lithe_lora_delta_grouped")
+
+
+def prepare_packed_group(xs: Sequence[torch.Tensor], ys: Sequence[torch.Tensor], bank_words: torch.Tensor,
+                         offsets: Sequence[Tuple[int, int]], num_levels: int,
+                         pools: Tuple[torch.Tensor, torch.Tensor], slots: torch.Tensor, rank: int, scaling: float,
+                         workspace: torch.Tensor, accumulate: bool = True) -> PreparedGroup:
+    """Prepared grouped index-resident deltas of the modules at ``offsets`` [(a_off, b_off)] of a
+    packed bank, module m reading ``xs[m]`` and updating ``ys[m]``."""
+    lut_a = _hip.lut_from_pools(pools[0], xs[0].dtype)
+    lut_b = _hip.lut_from_pools(pools[1], xs[0].dtype)
+    f = _delta.indexed_factors(_delta.packed_source(bank_words, num_levels, 0),
+                               _delta.packed_source(bank_words, num_levels, 0), lut_a, lut_b)
+    sl = slots.to(device=xs[0].device, dtype=torch.int32).reshape(-1, 1).contiguous()
+    return PreparedGroup(xs, ys, f, offsets, _delta.routes(sl), rank, [scaling] * len(xs), workspace, accumulate,
+                         keep=(sl, bank_words))

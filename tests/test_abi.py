@@ -40,7 +40,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_constants_match_header():
     d = _defines()
     assert d["LITHE_OK"] == _hip.OK
-    for n in ("NULL", "SHAPE", "ALIGN", "DTYPE", "RANGE", "WORKSPACE", "HIP", "LEVELS", "UNSUPPORTED"):
+    for n in ("NULL", "SHAPE", "ALIGN", "DTYPE", "RANGE", "WORKSPACE", "HIP", "LEVELS", "UNSUPPORTED", "OVERLAP"):
         assert d[f"LITHE_ERR_{n}"] == getattr(_hip, f"ERR_{n}"), n
     for n in ("BF16", "F32", "F16", "I16", "I32", "I64", "U16"):
         assert d[f"LITHE_DT_{n}"] == getattr(_hip, f"DT_{n}"), n
@@ -60,7 +60,7 @@ def test_struct_layouts_match_header_sizes():
 def test_version_and_status_strings():
     lib = _hip.load()
     assert lib.lithe_abi_version() == 1
-    for code in range(0, -10, -1):
+    for code in range(0, -11, -1):
         s = lib.lithe_status_string(code).decode()
         assert s and "unknown" not in s.lower(), (code, s)
     assert "unknown" in lib.lithe_status_string(-99).decode().lower()
@@ -318,4 +318,61 @@ def test_noalloc_delta_argument_errors_before_any_launch():
     assert lib.lithe_lora_workspace_bytes(14, 37_449, 3072, 3072, 16, 1, _hip.DT_BF16) - 256 <= _hip.STATIC_SCRATCH_BYTES
     if not torch.cuda.is_available():
         assert call(n_batch=14, seq=37_449) == _hip.ERR_HIP
+    del words
+
+
+def test_grouped_argument_errors_and_workspace_bytes():
+    """lithe_lora_delta_grouped: per-module checks of lithe_lora_delta, the module limit, indexed
+    factors only, the workspace of one intermediate per distinct input; no call reaches a launch."""
+    lib = _hip.load()
+    f, words = _indexed(n_slots=4, d_in=128, d_out=64)
+    slot = np.zeros(2, dtype=np.int32)
+    route = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=None, slot_scale=None, n_route=1)
+
+    def mods(n, **kw):
+        arr = (_hip.Module * max(1, n))()
+        for i in range(n):
+            arr[i].x, arr[i].y = kw.get("x", 1 << 12), kw.get("y", 1 << 13)
+            if kw.get("distinct", False) and arr[i].y:
+                arr[i].y += i << 16
+            arr[i].seq, arr[i].d_in, arr[i].d_out = kw.get("seq", 8), 128, kw.get("d_out", 64)
+            arr[i].a_block_off, arr[i].b_block_off, arr[i].out_scale = 0, 32, 1.0
+        return arr
+
+    def call(arr, n, fa=f, wsb=1 << 20, n_batch=2, ws=1 << 12):
+        return lib.lithe_lora_delta_grouped(n, arr, _hip.DT_BF16, _hip.DT_BF16, n_batch, 1, 16,
+                                            ctypes.byref(fa) if fa else None, ctypes.byref(route),
+                                            ctypes.c_void_p(ws), wsb, None)
+
+    assert call(None, 2) == _hip.ERR_NULL
+    assert call(mods(2), 2, fa=None) == _hip.ERR_NULL
+    assert call(mods(1), 0) == _hip.ERR_SHAPE
+    assert call(mods(9), 9) == _hip.ERR_SHAPE                                 # more than 8 modules
+    dense = _hip.Factors()
+    dense.kind = _hip.FACTOR_DENSE
+    assert call(mods(2), 2, fa=dense) == _hip.ERR_UNSUPPORTED
+    assert call(mods(2, x=(1 << 12) + 8), 2) == _hip.ERR_ALIGN               # x not 16-byte aligned
+    assert call(mods(2, d_out=6), 2) == _hip.ERR_ALIGN                       # d_out * rank % 64
+    assert call(mods(2, y=0), 2) == _hip.ERR_NULL
+    assert call(mods(2, distinct=True), 2, wsb=256) == _hip.ERR_WORKSPACE
+    assert call(mods(2), 2, ws=0) == _hip.ERR_WORKSPACE
+    assert call(mods(2, seq=0), 2) == _hip.OK                                # nothing to do
+    assert call(mods(2), 2, n_batch=0) == _hip.OK
+    same_y = mods(2)                                                          # both write one output
+    assert call(same_y, 2) == _hip.ERR_OVERLAP
+    part = mods(2)
+    part[1].y = (1 << 13) + 2 * 8 * 64 * 2 - 16                               # the last 16 bytes overlap
+    assert call(part, 2) == _hip.ERR_OVERLAP
+    far = mods(1)
+    far[0].b_block_off = 10_000                                               # B past the end of a slot
+    assert call(far, 1) == _hip.ERR_SHAPE
+    # two modules over one x share one intermediate of 2 x 16 ranks; a third x adds its own
+    wb = lib.lithe_lora_grouped_workspace_bytes
+    arr = mods(3)
+    arr[2].x = 1 << 14
+    rows = 2 * 8
+    assert wb(2, 3, arr, 16, 1, _hip.DT_BF16) == 256 + ((rows * 2 * 16 * 2 + 255) // 256) * 256 + \
+        ((rows * 16 * 2 + 255) // 256) * 256
+    assert wb(2, 9, arr, 16, 1, _hip.DT_BF16) == _hip.ERR_SHAPE
+    assert wb(2, 3, arr, 16, 9, _hip.DT_BF16) == _hip.ERR_SHAPE                # 9 rank groups
     del words
