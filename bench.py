@@ -8,9 +8,13 @@ bit-packed 9-bit indices (24.0 GB resident). Each module adds its delta into a
 precomputed base output: y += (x A_j^T) B_j^T with A_j, B_j decoded on the fly
 inside the kernels. Inputs are synthetic (x, y ~ N(0, 1); uniformly random
 9-bit fields) and already resident in HBM; x / y buffers rotate so the 256 MB
-Infinity Cache cannot serve a module from a previous module's data.
+Infinity Cache cannot serve a module from a previous module's data. The
+independent linears of each block stage (the image and text projections, the two
+attention outputs, the two up and the two down projections, a single block's
+q / k / v) run as one grouped call: one shrink and one expand launch per stage,
+114 calls per sweep (``--config flux342``: one call per module).
 
-    python bench.py [--steps K] [--warmup W] [--config flux342|qkv|decoded|ffn|hb|decode|ingest|encode] [--rank 16|64]
+    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|ffn|hb|decode|ingest|encode] [--rank 16|64]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -680,7 +684,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="flux342",
+    ap.add_argument("--config", default="grouped",
                     choices=["flux342", "qkv", "grouped", "fused", "decoded", "ffn", "hb", "decode", "ingest",
                              "encode"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
