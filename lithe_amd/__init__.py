@@ -7,8 +7,8 @@ ABI of ``include/lithe_amd.h``.
 """
 from .codebook import (BLOCK_SIZE, K, N_BITS, NUM_LEVELS, SIGMA_A, SIGMA_B, build_pools, codebook_sha256,
                        codewords, twin_pools)
-from .convert import decode_factors, from_dense_lora, to_lora_state_dict
 from .fileio import LitheAdapter, load_lithe, read_header, save_lithe
+from .kernels.packed import decode_factors
 from .module import FLUX_TARGET_MODULES, LitheLinear, TwinCodebook, inject_lithe, lithe_layers
 
 __version__ = "0.1.0"
@@ -16,7 +16,7 @@ __version__ = "0.1.0"
 __all__ = [
     "BLOCK_SIZE", "K", "N_BITS", "NUM_LEVELS", "SIGMA_A", "SIGMA_B",
     "build_pools", "codebook_sha256", "codewords", "twin_pools",
-    "decode_factors", "from_dense_lora", "to_lora_state_dict",
+    "decode_factors",
     "LitheAdapter", "load_lithe", "read_header", "save_lithe",
     "FLUX_TARGET_MODULES", "LitheLinear", "TwinCodebook", "inject_lithe", "lithe_layers",
 ]

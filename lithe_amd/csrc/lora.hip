@@ -362,9 +362,11 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
                                              const float *mid_scale, const float *out_scale, void *workspace,
                                              int64_t workspace_bytes, void *stream) {
     if (!f || !y || !d_out || !out_scale) return LITHE_ERR_NULL;
-    if (n_mod < 1) return LITHE_ERR_SHAPE;
+    if (n_mod < 1 || n_mod > kMaxGroups) return LITHE_ERR_SHAPE;
     const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
-    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, n_mod, workspace);
+    // replicated form: a workgroup carries one module's rank groups; the stacked form carries all
+    const bool stacked = getenv("LITHE_SHARED_X_STACKED") != nullptr;
+    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, stacked ? n_mod : 1, workspace);
     if (rc || n_batch == 0 || seq == 0) return rc;
     const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
     const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
@@ -402,7 +404,6 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
     // Shrink: replicated (one single-module workgroup per tile and module, x shared through the
     // Infinity Cache) unless LITHE_SHARED_X_STACKED asks for the module-stacked kernel (all
     // modules' A rows as rank groups of one workgroup).
-    const bool stacked = getenv("LITHE_SHARED_X_STACKED") != nullptr;
     Plan pshrink = ps;
     if (stacked) {
         for (int g = 0; g < kMaxGroups; ++g) a.a_goff[g] = f[std::min(g / G1, n_mod - 1)].a_idx.block_off;

@@ -240,7 +240,9 @@ _workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised scratch for lithe_lora_delta, one per (device, stream), grown on demand."""
+    """Zero-initialised scratch for lithe_lora_delta, one per (device, stream), grown on demand.
+    A grown workspace starts with the error word of the one it replaces (copied on the same
+    stream), so errors recorded before the growth are still reported."""
     dev = torch.device(device)
     key = (dev.index if dev.index is not None else torch.cuda.current_device(),
            torch.cuda.current_stream(dev).cuda_stream)
@@ -249,7 +251,10 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         size = max(int(nbytes), 1 << 20)
         if ws is not None:
             size = max(size, 2 * ws.numel())
-        ws = torch.zeros(size, dtype=torch.uint8, device=dev)
+        grown = torch.zeros(size, dtype=torch.uint8, device=dev)
+        if ws is not None:
+            grown[:4].copy_(ws[:4])
+        ws = grown
         _workspaces[key] = ws
     return ws
 

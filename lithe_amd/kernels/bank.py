@@ -34,6 +34,7 @@ class PackedBank:
         # int64 storage (torch has more kernels for it); the bits are the uint64 words.
         self._words = torch.zeros((max(1, int(capacity)), layout.num_words), dtype=torch.int64, device=self.device)
         self.num_slots = 0
+        self.generation = 0                # bumped by every write into the words (cached results are stale)
         self._free: List[int] = []        # freed slot ids, ascending
         self._stage = None                 # (pinned stream, device stream, error word, copy event)
 
@@ -59,6 +60,7 @@ class PackedBank:
         return [self._words[i].view(torch.uint64) for i in range(self.num_slots)]
 
     def reserve(self, capacity: int) -> None:
+        self.generation += 1
         if capacity <= self._words.shape[0]:
             return
         grown = torch.zeros((capacity, self.layout.num_words), dtype=torch.int64, device=self.device)
@@ -67,6 +69,7 @@ class PackedBank:
 
     def add(self, words: torch.Tensor) -> int:
         """Append one adapter's packed words (CPU or GPU); returns its slot id."""
+        self.generation += 1
         if words.numel() != self.layout.num_words:
             raise ValueError(f"expected {self.layout.num_words} words, got {words.numel()}")
         if self.num_slots == self._words.shape[0]:
@@ -80,6 +83,7 @@ class PackedBank:
 
     def fill_to(self, n: int, template_slot: int = 0) -> None:
         """Grow to ``n`` slots by copying a resident slot (distinct rows, same content)."""
+        self.generation += 1
         if n <= self.num_slots:
             return
         self.reserve(n)
@@ -88,6 +92,7 @@ class PackedBank:
 
     def fill_random(self, n: int, generator: Optional[torch.Generator] = None) -> None:
         """Grow to ``n`` slots of uniformly random 9-bit fields (padding fields of the last word zero)."""
+        self.generation += 1
         self.reserve(n)
         k = n - self.num_slots
         if k <= 0:
@@ -137,6 +142,7 @@ class PackedBank:
 
     # -------------------------------------------------------------- ingest
     def _target(self, slot: Optional[int]) -> int:
+        self.generation += 1
         if slot is None:
             return self.alloc()
         if not 0 <= slot < self.num_slots:

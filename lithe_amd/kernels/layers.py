@@ -28,27 +28,54 @@ from .sgmv import lora_delta_dense, per_sample_lora_delta
 Factor = Tuple[torch.Tensor, torch.Tensor, float]
 
 
+def replace_module(model: nn.Module, path: str, new: nn.Module) -> nn.Module:
+    """Put ``new`` at ``model.<path>`` (dotted, ModuleList indices included) and return the module
+    it replaces."""
+    owner_path, _, attr = path.rpartition(".")
+    owner = model.get_submodule(owner_path) if owner_path else model
+    old = getattr(owner, attr)
+    setattr(owner, attr, new)
+    return old
+
+
+def _stack_factors(factors: Sequence[Factor]):
+    """(A (n, r, d_in), B (n, d_out, r), scales (n,) fp32) of slot factors of one shape and device."""
+    a0, b0, _ = factors[0]
+    for a, b, _ in factors:
+        if a.shape != a0.shape or b.shape != b0.shape or a.device != a0.device or b.device != a0.device:
+            raise ValueError(f"slot factors must share one shape and device; got {tuple(a.shape)} / {tuple(b.shape)} "
+                             f"after {tuple(a0.shape)} / {tuple(b0.shape)}")
+    scales = torch.tensor([float(s) for _, _, s in factors], dtype=torch.float32, device=a0.device)
+    return torch.stack([a for a, _, _ in factors]), torch.stack([b for _, b, _ in factors]), scales
+
+
 class PerSampleLoRALinear(nn.Module):
-    """y = W x + scale_j * B_j A_j x for the slot j of every sample (decoded factors)."""
+    """y = W x + scale_j * B_j A_j x for the slot j of every sample (decoded factors).
+
+    ``factors`` holds the slot factors as installed (A (r, d_in), B (d_out, r), scale); the
+    kernels read them stacked, which is built once on the first forward after a change (or
+    installed directly by ``set_stacked``). ``kernel`` is kept for the reference's API: "sgmv"
+    and "loop" run the same HIP kernels.
+    """
 
     def __init__(self, base: nn.Linear, kernel: str = "sgmv"):
         super().__init__()
         if kernel not in ("sgmv", "loop"):
             raise ValueError(f"kernel must be 'sgmv' or 'loop', got {kernel!r}")
+        base.requires_grad_(False)
         self.base = base
-        for p in self.base.parameters():
-            p.requires_grad_(False)
-        self.kernel = kernel          # both names run the same HIP kernels
-        self.factors: List[Factor] = []
-        self.per_sample = False
+        self.kernel = kernel
         self.assign: Optional[torch.Tensor] = None
-        self._stacked = None
+        self.clear()
 
     def set_factors(self, factors: Sequence[Factor], per_sample: bool = True) -> None:
         """Install slot factors by reference (no copy); stacking happens lazily in forward."""
-        self.factors = list(factors)
+        self.factors: List[Factor] = list(factors)
         self.per_sample = per_sample
         self._stacked = None
+
+    def clear(self) -> None:
+        self.set_factors((), per_sample=False)
 
     def set_stacked(self, a: torch.Tensor, b: torch.Tensor, scales: torch.Tensor) -> None:
         """Install already stacked factors a (n, r, d_in), b (n, d_out, r) and scales (n,) -- e.g.
@@ -59,9 +86,6 @@ class PerSampleLoRALinear(nn.Module):
         self.per_sample = True
         self._stacked = (a.contiguous(), b.contiguous(), scales.to(device=a.device, dtype=torch.float32))
 
-    def clear(self) -> None:
-        self.set_factors([], per_sample=False)
-
     def _slots(self, bsz: int, device) -> torch.Tensor:
         if self.assign is not None:
             return self.assign.to(device=device, dtype=torch.int32)
@@ -69,10 +93,7 @@ class PerSampleLoRALinear(nn.Module):
 
     def _build_stacked(self):
         if self._stacked is None:
-            a = torch.stack([f[0] for f in self.factors]).contiguous()
-            b = torch.stack([f[1] for f in self.factors]).contiguous()
-            s = torch.tensor([float(f[2]) for f in self.factors], dtype=torch.float32, device=a.device)
-            self._stacked = (a, b, s)
+            self._stacked = _stack_factors(self.factors)
         return self._stacked
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -102,24 +123,33 @@ class PerSampleLoRALinear(nn.Module):
 
 
 class IndexLoRALinear(nn.Module):
-    """y = W x + per-sample delta decoded on the fly from resident index slots."""
+    """y = W x + per-sample delta decoded on the fly from resident index slots.
+
+    ``idx_a`` (n_slots, L, rank * d_in / 64) and ``idx_b`` (n_slots, L, d_out * rank / 64) are the
+    level-major indices of every slot (int16 and int32 are read as given, other integer dtypes
+    are converted to int32); ``pool_a`` / ``pool_b`` (L, 512, 64) are in the activation dtype.
+    """
 
     def __init__(self, base: nn.Linear, idx_a: torch.Tensor, idx_b: torch.Tensor,
                  pool_a: torch.Tensor, pool_b: torch.Tensor, rank: int, scaling: float):
         super().__init__()
+        base.requires_grad_(False)
         self.base = base
-        for p in self.base.parameters():
-            p.requires_grad_(False)
-        # (n_slots, L, n_blocks) int32; pools (L, K, block) in the activation dtype
-        self.register_buffer("idx_a", idx_a.to(torch.int32), persistent=False)
-        self.register_buffer("idx_b", idx_b.to(torch.int32), persistent=False)
-        self.register_buffer("pool_a", pool_a, persistent=False)
-        self.register_buffer("pool_b", pool_b, persistent=False)
         self.rank = int(rank)
         self.d_out = base.out_features
         self.scaling = float(scaling)
         self.assign: Optional[torch.Tensor] = None
         self._bank = None          # (PackedBank, a_off, b_off) for bank-backed layers
+        idx = {}
+        for name, t, blocks in (("idx_a", idx_a, -(-self.rank * base.in_features // 64)),
+                                ("idx_b", idx_b, -(-self.d_out * self.rank // 64))):
+            if t.dtype not in (torch.int16, torch.int32):
+                t = t.to(torch.int32)
+            if t.numel() and (t.dim() != 3 or t.shape[1] != pool_a.shape[0] or t.shape[2] != blocks):
+                raise ValueError(f"{name} must be (n_slots, {pool_a.shape[0]}, {blocks}), got {tuple(t.shape)}")
+            idx[name] = t
+        for name, t in (("idx_a", idx["idx_a"]), ("idx_b", idx["idx_b"]), ("pool_a", pool_a), ("pool_b", pool_b)):
+            self.register_buffer(name, t, persistent=False)
 
     @classmethod
     def from_bank(cls, base: nn.Linear, bank, name: str, dtype: Optional[torch.dtype] = None) -> "IndexLoRALinear":
@@ -187,17 +217,14 @@ class IndexLoRALinear(nn.Module):
 def wrap_linears(model: nn.Module, paths: Iterable[str],
                  factory: Callable[[str, nn.Linear], nn.Module]) -> Dict[str, nn.Module]:
     """Replace ``model.<path>`` (an ``nn.Linear``) by ``factory(path, linear)`` for every path."""
-    wrapped = {}
+    wrapped: Dict[str, nn.Module] = {}
     for path in paths:
-        base = model.get_submodule(path)
-        if not isinstance(base, nn.Linear):
+        linear = model.get_submodule(path)
+        if not isinstance(linear, nn.Linear):
             raise TypeError(f"{path} is not nn.Linear")
-        parent_name, _, child = path.rpartition(".")
-        parent = model.get_submodule(parent_name) if parent_name else model
-        module = factory(path, base)
-        setattr(parent, child, module)
-        wrapped[path] = module
+        wrapped[path] = factory(path, linear)
+        replace_module(model, path, wrapped[path])
     return wrapped
 
 
-__all__ = ["IndexLoRALinear", "PerSampleLoRALinear", "wrap_linears", "per_sample_lora_delta"]
+__all__ = ["IndexLoRALinear", "PerSampleLoRALinear", "wrap_linears", "replace_module", "per_sample_lora_delta"]

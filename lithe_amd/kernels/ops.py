@@ -5,7 +5,7 @@ with the delta as one opaque op that mutates the base output in place.
   y += delta of the module whose A / B blocks start at ``a_off`` / ``b_off`` of the packed bank
   ``words`` (n_slots, n_words); sample i uses slot ``slots[i, 0]``.
 * ``lithe_amd::index_lora_delta_(x, y, idx_a, idx_b, pool_a, pool_b, slots, rank, scaling)``:
-  the same over level-major int32 index stacks (n_slots, L, n_blocks) -- ``IndexLoRALinear``
+  the same over level-major int16 or int32 index stacks (n_slots, L, n_blocks) -- ``IndexLoRALinear``
   built from tensors (``lithe/kernels/layers.py:97-131``).
 
 Both run ``lithe_lora_delta`` with the rounding of ``out + delta * scaling``

@@ -423,3 +423,17 @@ def split_decoded(out: torch.Tensor, layout: PackedLayout) -> Dict[str, Tuple[to
     chunks = out.reshape(-1)[:total].split(sizes)
     return {name: (chunks[where[2 * i]].view(shapes[2 * i]), chunks[where[2 * i + 1]].view(shapes[2 * i + 1]))
             for i, name in enumerate(layout.names)}
+
+
+def decode_factors(ad, device="cuda", dtype: torch.dtype = torch.float32) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
+    """Every factor of an index adapter decoded on the GPU: {module: (A (r, d_in), B (d_out, r))}.
+
+    The adapter is packed in its own layout, every block decoded in one launch (``dtype`` fp32:
+    the reference's fp32 decode, ``lithe/quant.py:74-92``, bit for bit) and the result split
+    into per-module views of one buffer."""
+    from .. import codebook as cb
+    words, layout = pack_adapter(ad)
+    pools = (cb.build_pools(ad.sigma_a, ad.block_size, ad.n_bits).to(device),
+             cb.build_pools(ad.sigma_b, ad.block_size, ad.n_bits).to(device))
+    out = decode_packed(words.view(torch.int64).to(device), layout, *pools, dtype=dtype)
+    return split_decoded(out, layout)

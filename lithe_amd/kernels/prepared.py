@@ -28,6 +28,13 @@ def shared_workspace(device, nbytes: int) -> torch.Tensor:
     return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+def shared_x_workspace_bytes(x_shape, d_outs: Sequence[int], rank: int, n_route: int, x_dtype: torch.dtype) -> int:
+    """Workspace of ``lithe_lora_delta_shared_x``: the 256-byte head and one rank-r intermediate
+    row of every module per token (the layout of a grouped call whose modules share one x)."""
+    b, m, d_in = x_shape
+    return group_workspace_bytes([(m, d_in, d) for d in d_outs], [0] * len(d_outs), b, rank, n_route, x_dtype)
+
+
 class PreparedDelta:
     """y <- delta(x) for fixed tensors; see ``lithe_lora_delta`` in include/lithe_amd.h."""
 
@@ -110,7 +117,7 @@ class PreparedSharedX:
             raise ValueError("one factor set and one scale per output")
         if any(y.shape[:2] != x.shape[:2] or y.dtype != ys[0].dtype for y in ys):
             raise ValueError("every y must be (B, M, d_out) like x, in one dtype")
-        need = workspace_bytes(tuple(x.shape), max(y.shape[2] for y in ys), rank, route.n_route * n, x.dtype)
+        need = shared_x_workspace_bytes(tuple(x.shape), [y.shape[2] for y in ys], rank, route.n_route, x.dtype)
         if workspace.numel() < need:
             raise ValueError(f"workspace holds {workspace.numel()} bytes, the call needs {need}")
         self.x, self.ys, self.workspace = x, list(ys), workspace

@@ -17,6 +17,7 @@ Model loading and rendering (diffusers pipelines) are not part of this package.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Dict, List, Optional, Sequence
 
 import numpy as np
@@ -25,8 +26,8 @@ from torch import nn
 
 from .kernels import _delta, _hip
 from .kernels.bank import PackedBank
-from .kernels.layers import IndexLoRALinear, PerSampleLoRALinear, wrap_linears
-from .kernels.prepared import workspace_bytes
+from .kernels.layers import IndexLoRALinear, PerSampleLoRALinear, replace_module, wrap_linears
+from .kernels.prepared import shared_x_workspace_bytes
 from .module import FLUX_TARGET_MODULES
 from . import codebook as cb
 
@@ -72,9 +73,10 @@ class SharedInputGroup:
 
     The first member called with an input computes every member's base output, adds all
     their deltas with one shrink over x (``lithe_lora_delta_shared_x``), returns its own and
-    keeps the others until their members are called with the same input (same storage,
-    shape, dtype and version counter). A member called with another input falls back to
-    computing the group for that input, so results never depend on the call order.
+    keeps the others until their members are called with the same input tensor (the same
+    object at the same version counter, under the same routing tensor and bank generation).
+    Any other call recomputes the group and drops what was pending, so results never depend on
+    the call order.
     """
 
     def __init__(self, layers: Sequence[IndexLoRALinear]):
@@ -101,7 +103,7 @@ class SharedInputGroup:
         fs = [l._factors(x.dtype) for l in self.layers]
         n = len(self.layers)
         lib = _hip.load()
-        need = workspace_bytes(tuple(x3.shape), max(o.shape[2] for o in o3), lead.rank, n, x.dtype)
+        need = shared_x_workspace_bytes(tuple(x3.shape), [o.shape[2] for o in o3], lead.rank, 1, x.dtype)
         ws = _hip.workspace(x.device, need)
         fa = (_hip.Factors * n)(*fs)
         ya = (ctypes.c_void_p * n)(*[o.data_ptr() for o in o3])
@@ -115,13 +117,21 @@ class SharedInputGroup:
         _hip.check(rc, "lithe_lora_delta_shared_x")
         return [o.squeeze(1) if squeeze else o for o in o3]
 
+    def _state(self, x: torch.Tensor):
+        """What the pending outputs were computed from, besides the input object itself: its
+        version, the routing tensor and its version, and the bank's generation (bumped by every
+        write into a slot)."""
+        a = self.layers[0].assign
+        return (x._version, id(a), getattr(a, "_version", None), self.layers[0]._bank[0].generation)
+
     def output(self, i: int, x: torch.Tensor) -> torch.Tensor:
-        key = (x.data_ptr(), tuple(x.shape), x.dtype, x._version)
-        if key == self._key and self._pending[i] is not None:
+        state = self._state(x)
+        same = self._key is not None and self._key[0]() is x and self._key[1] == state
+        if same and self._pending[i] is not None:
             out, self._pending[i] = self._pending[i], None
             return out
         outs = self._compute(x)
-        self._key = key
+        self._key = (weakref.ref(x), state)
         self._pending = [o if j != i else None for j, o in enumerate(outs)]
         return outs[i]
 
@@ -167,11 +177,8 @@ def wrap_bank(model: nn.Module, bank: PackedBank, module_set: str = "all", dtype
                     continue
                 group = SharedInputGroup([wrapped[m] for m in members])
                 for i, m in enumerate(members):
-                    stand_in = SharedInputMember(group, i)
-                    parent_name, _, child = m.rpartition(".")
-                    parent = model.get_submodule(parent_name) if parent_name else model
-                    setattr(parent, child, stand_in)
-                    wrapped[m] = stand_in
+                    wrapped[m] = SharedInputMember(group, i)
+                    replace_module(model, m, wrapped[m])
     return wrapped
 
 

@@ -211,3 +211,21 @@ def test_decode_rank64_flux_layout_staged_sides():
     out2 = torch.empty_like(out)
     _decode(_delta.packed_source(w.view(1, -1), layout.num_levels, 0), n, buf[1:], pa_t, pb_t, out2)
     assert torch.equal(out2, out)
+
+
+def test_decode_factors_equals_oracle_decode():
+    """lithe_amd.decode_factors (one packed decode of the whole adapter, split into per-module
+    views) gives every factor of the oracle's fp32 level-order decode bit for bit, the
+    non-multiple-of-64 module included."""
+    import lithe_amd
+    from helpers import SMALL, random_adapter
+    ad = random_adapter(SMALL, rank=16, seed=31)
+    got = lithe_amd.decode_factors(ad)
+    pa, pb = ocb.twin_pools()
+    for m in ad.modules:
+        a, b = got[m["name"]]
+        want_a = odec.decode(ad.indices[m["name"]]["A"], m["shape_a"], pa)
+        want_b = odec.decode(ad.indices[m["name"]]["B"], m["shape_b"], pb)
+        assert a.dtype == torch.float32 and tuple(a.shape) == tuple(m["shape_a"])
+        assert np.array_equal(a.cpu().numpy().view(np.uint32), want_a.view(np.uint32)), m["name"]
+        assert np.array_equal(b.cpu().numpy().view(np.uint32), want_b.view(np.uint32)), m["name"]

@@ -134,3 +134,21 @@ def test_two_streams_at_once_match_one_stream():
         for i, (g, e) in enumerate(zip(got, want)):
             assert torch.equal(g, e), (rep, i)
     assert _hip.workspace_errors() == 0
+
+
+def test_grown_workspace_keeps_recorded_errors():
+    """A bad slot id is recorded in the stream's workspace; a larger call that grows the workspace
+    afterwards keeps the recorded bit (workspace_errors reports it once, then it is cleared)."""
+    from lithe_amd.kernels import _hip, packed_lora_delta
+    _, bank = _bank()
+    pools = (bank.pool_a.bfloat16(), bank.pool_b.bfloat16())
+    _, _, _, a_off, b_off = bank.layout.module("q")
+    _hip.workspace_errors()                                          # start clean
+    small = torch.randn(1, 16, 3072, device="cuda").bfloat16()
+    packed_lora_delta(small, bank.words, a_off, b_off, 3, pools, torch.tensor([bank.num_slots], device="cuda"),
+                      16, 3072, 1.0)
+    big = torch.randn(8, 20_000, 3072, device="cuda").bfloat16()    # 5.1 MB of intermediate: a new workspace
+    packed_lora_delta(big, bank.words, a_off, b_off, 3, pools, torch.zeros(8, dtype=torch.int32, device="cuda"),
+                      16, 3072, 1.0)
+    assert _hip.workspace_errors() == 1
+    assert _hip.workspace_errors() == 0

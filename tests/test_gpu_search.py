@@ -121,43 +121,3 @@ def test_quant_nearest_index_matches_oracle():
     want, proj = osr.nearest_index(x)
     clear = np.abs(proj).min(axis=1) > 1e-5 * float(np.abs(x).max())
     assert clear.mean() > 0.99 and np.array_equal(got[clear], want[clear])
-
-
-def test_dense_lora_encoding_round_trip():
-    """tests/test_module.py:115-127 of the reference, restated: factors that are exact lattice
-    points survive from_dense_lora -> decode_factors (B exactly; A's equal level scales allow
-    other index triples with the same sum, so A is checked on its reconstruction)."""
-    rng = np.random.default_rng(0)
-    pa, pb = ocb.twin_pools()
-    true_a = odec.decode(rng.integers(0, 512, (3, 8 * 96 // 64)), (8, 96), pa)
-    true_b = odec.decode(rng.integers(0, 512, (3, 160 * 8 // 64)), (160, 8), pb)
-    sd = {"transformer.attn.to_q.lora_A.weight": torch.from_numpy(true_a),
-          "transformer.attn.to_q.lora_B.weight": torch.from_numpy(true_b)}
-    ad = lithe_amd.from_dense_lora(sd)
-    assert ad.rank == 8 and ad.alpha == 8.0 and [m["name"] for m in ad.modules] == ["attn.to_q"]
-    a, b = lithe_amd.decode_factors(ad)["attn.to_q"]
-    assert np.allclose(a.cpu().numpy(), true_a, atol=1e-7)
-    assert np.array_equal(b.cpu().numpy(), true_b)
-
-
-def test_lora_state_dict_round_trip_and_alpha_folding():
-    """to_lora_state_dict folds alpha / r into B (lithe/convert.py:32-56); encoding the dense
-    state dict again gives the adapter's B indices back (pool B levels are separable)."""
-    from helpers import random_adapter
-    ad = random_adapter([("blk.attn.to_k", 128, 192), ("blk.ff.net.2", 256, 64)], rank=16, seed=9)
-    ad.alpha = 16.0
-    sd = lithe_amd.to_lora_state_dict(ad, dtype=torch.float32)
-    assert sorted(sd) == sorted(f"transformer.{n}.lora_{s}.weight" for n in ("blk.attn.to_k", "blk.ff.net.2")
-                                for s in "AB")
-    pa, pb = ocb.twin_pools()
-    for m in ad.modules:
-        want_b = odec.decode(ad.indices[m["name"]]["B"].astype(np.int64), m["shape_b"], pb)
-        assert np.array_equal(sd[f"transformer.{m['name']}.lora_B.weight"].numpy(), want_b)
-    back = lithe_amd.from_dense_lora(sd)
-    for m in ad.modules:
-        assert np.array_equal(back.indices[m["name"]]["B"], ad.indices[m["name"]]["B"])
-    # alpha folding: with alpha = r / 2 the state dict's B is halved
-    ad.alpha = 8.0
-    sd2 = lithe_amd.to_lora_state_dict(ad, dtype=torch.float32)
-    k = "transformer.blk.ff.net.2.lora_B.weight"
-    assert torch.equal(sd2[k], sd[k] * 0.5)

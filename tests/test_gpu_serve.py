@@ -152,6 +152,11 @@ def test_lithe_linear_inference():
         got = to_np(model(x.cuda()))
     want = odelta.lithe_linear(to_np(x), base_out, a_hat, b_hat, 0.5, "bf16")
     assert rel(got, want) < 2e-3
+    # the codebook's GPU encode returns every B index of the decoded factor (pool B's level scales
+    # are separable) and reconstructs it exactly
+    idx_b, b_rec = layer.codebook.encode(bh, "B")
+    assert np.array_equal(idx_b.cpu().numpy(), ad.indices["fc"]["B"].astype(np.int64))
+    assert torch.equal(b_rec, bh)
 
 
 @pytest.mark.parametrize("n_routes,rank,d_out", [(2, 16, 200), (6, 16, 200), (8, 16, 328), (2, 32, 264), (5, 8, 96)])

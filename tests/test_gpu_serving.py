@@ -99,3 +99,43 @@ def test_torch_compile_traces_the_lithe_ops():
         compiled = torch.compile(model, backend="aot_eager", fullgraph=True)(h, c)
     assert explain.graph_break_count == 0
     assert torch.equal(compiled, eager)
+
+
+def test_shared_input_group_rank64_and_stale_state():
+    """Shared-input groups at rank 64 (4 rank groups per module, 12 for a q / k / v group: each
+    workgroup carries one module's groups) match the unfused model; a pending member output is
+    not reused after the routing or a bank slot changed, nor for another tensor."""
+    torch.manual_seed(4)
+    model = ToyFlux().cuda().bfloat16()
+    mods = target_modules(model)
+    ads = [random_adapter(mods, rank=64, seed=400 + s) for s in range(3)]
+    bank, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bank.add(w)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    h = torch.randn(2, 48, 256, device="cuda", generator=g).bfloat16()
+    c = torch.randn(2, 16, 256, device="cuda", generator=g).bfloat16()
+    m1, m2 = copy.deepcopy(model), copy.deepcopy(model)
+    w1 = serving.wrap_bank(m1, bank)
+    w2 = serving.wrap_bank(m2, bank, fuse_shared_inputs=True)
+    a0 = torch.tensor([2, 0], dtype=torch.int32, device="cuda")
+    serving.set_assign(w1, a0)
+    serving.set_assign(w2, a0)
+    with torch.no_grad():
+        assert rel(to_np(m2(h, c)), to_np(m1(h, c))) < 2e-3
+        attn1, attn2 = m1.transformer_blocks[0].attn, m2.transformer_blocks[0].attn
+        attn2.to_q(h)                                    # k and v now pending for (h, a0)
+        a1 = torch.tensor([1, 1], dtype=torch.int32, device="cuda")
+        serving.set_assign(w1, a1)
+        serving.set_assign(w2, a1)
+        assert rel(to_np(attn2.to_k(h)), to_np(attn1.to_k(h))) < 2e-3      # recomputed under a1
+        attn2.to_q(h)                                    # pending again, then slot 1 is rewritten
+        saved = bank.words[1].clone()
+        bank.words[1].copy_(bank.words[0])
+        bank.generation += 1
+        assert rel(to_np(attn2.to_v(h)), to_np(attn1.to_v(h))) < 2e-3
+        attn2.to_q(h)
+        h2 = h.clone()                                   # equal values, another tensor
+        bank.words[1].copy_(saved)
+        bank.generation += 1
+        assert rel(to_np(attn2.to_k(h2)), to_np(attn1.to_k(h2))) < 2e-3

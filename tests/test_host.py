@@ -178,3 +178,49 @@ def test_split_views_equal_per_module_slices():
         na, nb = sa[0] * sa[1], sb[0] * sb[1]
         assert torch.equal(st[name][0], buf[n_sel * ao * 64: n_sel * ao * 64 + n_sel * na].view(n_sel, *sa)), name
         assert torch.equal(st[name][1], buf[n_sel * bo * 64: n_sel * bo * 64 + n_sel * nb].view(n_sel, *sb)), name
+
+
+def test_attach_adapters_loads_every_adapter_in_order():
+    """attach_adapters on a CPU model: each layer's int16 stacks hold adapter i's indices at row i
+    (the stores grow past their capacity), scales are alpha / r; mismatched adapters are refused."""
+    from torch import nn
+
+    from helpers import random_adapter
+
+    class Two(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.a = nn.Linear(128, 64)
+            self.b = nn.Linear(64, 192)
+
+    ads = [random_adapter([("a", 128, 64), ("b", 64, 192)], rank=4, seed=s) for s in range(5)]
+    for i, ad in enumerate(ads):
+        ad.alpha = float(2 * i + 1)
+    model = Two()
+    router, layers = serve.attach_adapters(model, ads)
+    assert set(layers) == {"a", "b"} and model.a is layers["a"] and layers["a"].router is router
+    for name in ("a", "b"):
+        lay = layers[name]
+        assert lay.idx_a.shape[0] == lay.idx_b.shape[0] == 5 and lay.idx_a.dtype == torch.int16
+        for i, ad in enumerate(ads):
+            assert np.array_equal(lay.idx_a[i].numpy(), ad.indices[name]["A"].astype(np.int16))
+            assert np.array_equal(lay.idx_b[i].numpy(), ad.indices[name]["B"].astype(np.int16))
+        assert lay.scales.tolist() == [(2 * i + 1) / 4 for i in range(5)]
+    with pytest.raises(ValueError):
+        layers["a"].add_adapter(ads[0].indices["b"]["A"], ads[0].indices["b"]["B"], 1.0)
+    other = random_adapter([("a", 128, 64)], rank=4, seed=9)
+    with pytest.raises(ValueError):
+        serve.attach_adapters(Two(), [ads[0], other])
+    with pytest.raises(ValueError):
+        serve.attach_adapters(Two(), [])
+
+
+def test_target_match_is_a_whole_component_suffix():
+    """module._match: a path matches a target when it equals it or ends with '.' + target
+    (lithe/module.py:159-160), never inside a path component."""
+    t = ["attn.to_q", "ff.net.2"]
+    for path, want in [("attn.to_q", True), ("transformer_blocks.3.attn.to_q", True), ("xattn.to_q", False),
+                       ("to_q", False), ("single.attn.to_q.lora", False), ("blk.ff.net.2", True),
+                       ("blk.ff.net.20", False), ("blk.ff_context.net.2", False)]:
+        assert module._match(path, t) == want, path
+        assert module._match(path, t) == any(path == s or path.endswith("." + s) for s in t), path
