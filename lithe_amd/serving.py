@@ -8,6 +8,10 @@
   every layer at once). With ``fuse_shared_inputs`` the projections that read one input
   (``to_q`` / ``to_k`` / ``to_v``, ``add_q_proj`` / ``add_k_proj`` / ``add_v_proj``) share
   one shrink over x (``lithe_lora_delta_shared_x``).
+* ``stage_groups`` collects the independent linears of each FLUX block stage (image and text
+  projections, the two attention outputs, the two up and the two down projections) into
+  ``StageGroup`` objects that add all of a stage's deltas in one grouped call
+  (``lithe_lora_delta_grouped``), for a serving step that issues a stage at once.
 * ``wrap_decoded`` / ``install_per_sample`` / ``install_single`` are the decoded-mode
   counterparts (``serving/_common.py:268-281``), and ``install_decoded_bank`` installs the
   stacked factors of ``PackedBank.decode_stacked`` without per-module copies.
@@ -18,7 +22,7 @@ from __future__ import annotations
 
 import ctypes
 import weakref
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -159,6 +163,76 @@ class SharedInputMember(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self._group.output(self._index, x)
+
+
+# The independent linears of each stage of a FLUX block, in call order: a serving step can compute
+# a stage's base outputs and then add all of its deltas in one grouped call.
+STAGES = {
+    "proj": ("attn.to_q", "attn.to_k", "attn.to_v", "attn.add_q_proj", "attn.add_k_proj", "attn.add_v_proj"),
+    "out": ("attn.to_out.0", "attn.to_add_out"),
+    "up": ("ff.net.0.proj", "ff_context.net.0.proj"),
+    "down": ("ff.net.2", "ff_context.net.2"),
+}
+
+
+class StageGroup:
+    """Bank-backed layers of one block stage whose deltas run as one grouped call.
+
+    ``group(inputs)`` returns ``[layer_m.base(inputs[m]) + delta_m]`` for every member m: the base
+    GEMMs first, then one ``lithe_lora_delta_grouped`` launch pair over the whole stage (members
+    given the same input tensor, e.g. q / k / v, share its shrink). Routing is the first member's
+    ``assign`` (``set_assign`` gives every member the same).
+    """
+
+    def __init__(self, layers: Sequence[IndexLoRALinear]):
+        layers = [getattr(l, "layer", l) for l in layers]      # shared-input stand-ins carry their layer
+        if not 1 <= len(layers) <= _hip.MAX_GROUP_MODULES or any(l._bank is None for l in layers):
+            raise ValueError(f"a stage group holds 1 to {_hip.MAX_GROUP_MODULES} bank-backed layers")
+        bank = layers[0]._bank[0]
+        if any(l._bank[0] is not bank or l.rank != layers[0].rank for l in layers):
+            raise ValueError("grouped layers must share one bank and rank")
+        self.layers = layers
+
+    def __call__(self, inputs: Sequence[torch.Tensor]) -> List[torch.Tensor]:
+        if len(inputs) != len(self.layers):
+            raise ValueError(f"{len(self.layers)} inputs expected, got {len(inputs)}")
+        lead = self.layers[0]
+        bank = lead._bank[0]
+        squeeze = inputs[0].dim() == 2
+        outs = [l.base(x) for l, x in zip(self.layers, inputs)]
+        xs, ys = [], []
+        for i, (x, o) in enumerate(zip(inputs, outs)):
+            if (x.dim() == 2) != squeeze or x.shape[0] != inputs[0].shape[0]:
+                raise ValueError("every input must have the batch size and rank of the first")
+            # one contiguous 3-D view per distinct input tensor, so shared shrinks stay shared
+            first = next(j for j in range(i + 1) if inputs[j] is x)
+            xs.append(xs[first] if first < i else (x.unsqueeze(1) if squeeze else x).contiguous())
+            ys.append(o.unsqueeze(1) if squeeze else o)
+        bsz = xs[0].shape[0]
+        slots = (torch.zeros((bsz, 1), dtype=torch.int32, device=xs[0].device) if lead.assign is None
+                 else lead.assign.to(device=xs[0].device, dtype=torch.int32).reshape(-1, 1).contiguous())
+        torch.ops.lithe_amd.bank_lora_delta_grouped_(
+            xs, ys, bank.words, [l._bank[1] for l in self.layers], [l._bank[2] for l in self.layers],
+            lead.pool_a, lead.pool_b, slots, lead.rank, [l.scaling for l in self.layers])
+        return outs
+
+
+def stage_groups(wrapped: Dict[str, nn.Module]) -> Dict[Tuple[str, str], StageGroup]:
+    """The FLUX block stages among bank-backed wrappers: {(block prefix, stage): StageGroup} for
+    every stage of ``STAGES`` whose linears are all wrapped (a single block's q / k / v form its
+    "proj" stage), members in call order."""
+    groups: Dict[Tuple[str, str], StageGroup] = {}
+    for path in wrapped:
+        for stage, suffixes in STAGES.items():
+            if not path.endswith(suffixes[0]):
+                continue
+            prefix = path[: -len(suffixes[0])]
+            full = [prefix + s for s in suffixes]
+            if all(m in wrapped for m in full):
+                groups[(prefix, stage)] = StageGroup([wrapped[m] for m in full])
+            elif stage == "proj" and all(m in wrapped for m in full[:3]) and not any(m in wrapped for m in full[3:]):
+                groups[(prefix, stage)] = StageGroup([wrapped[m] for m in full[:3]])
+    return groups
 
 
 def wrap_bank(model: nn.Module, bank: PackedBank, module_set: str = "all", dtype: Optional[torch.dtype] = None,

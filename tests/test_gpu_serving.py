@@ -139,3 +139,44 @@ def test_shared_input_group_rank64_and_stale_state():
         bank.words[1].copy_(saved)
         bank.generation += 1
         assert rel(to_np(attn2.to_k(h2)), to_np(attn1.to_k(h2))) < 2e-3
+
+
+def _grouped_double(block, groups, prefix, h, c):
+    """DoubleBlock.forward of tests/toy_flux.py with every stage's deltas in one grouped call."""
+    q, k, v, cq, ck, cv = groups[(prefix, "proj")]([h, h, h, c, c, c])
+    ho, co = groups[(prefix, "out")]([q * torch.sigmoid(k) + v, cq * torch.sigmoid(ck) + cv])
+    h, c = h + ho, c + co
+    up_h, up_c = groups[(prefix, "up")]([h, c])
+    act = block.ff.net[1]
+    dn_h, dn_c = groups[(prefix, "down")]([act(up_h), act(up_c)])
+    return h + dn_h, c + dn_c
+
+
+def _grouped_forward(model, groups, h, c):
+    for i, b in enumerate(model.transformer_blocks):
+        h, c = _grouped_double(b, groups, f"transformer_blocks.{i}.", h, c)
+    h = torch.cat([c, h], dim=1)
+    for i, b in enumerate(model.single_transformer_blocks):
+        q, k, v = groups[(f"single_transformer_blocks.{i}.", "proj")]([h, h, h])
+        h = h + q * torch.sigmoid(k) + v
+    return h
+
+
+def test_stage_groups_equal_per_module_layers_and_compile(monkeypatch):
+    """A forward that issues each block stage as one grouped call (serving.stage_groups) equals the
+    wrapped model's per-module forward bit for bit when both plans split K the same way, and
+    torch.compile traces it (the grouped delta is one lithe_amd:: op) with no graph break."""
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    model, ads, bank, h, c = _setup(6)
+    w = serving.wrap_bank(model, bank)
+    serving.set_assign(w, torch.tensor([3, 1, 0], dtype=torch.int32, device="cuda"))
+    groups = serving.stage_groups(w)
+    with torch.no_grad():
+        per_module = model(h, c)
+        grouped = _grouped_forward(model, groups, h, c)
+        assert torch.equal(grouped, per_module)
+        torch._dynamo.reset()
+        explain = torch._dynamo.explain(_grouped_forward)(model, groups, h, c)
+        compiled = torch.compile(_grouped_forward, backend="aot_eager", fullgraph=True)(model, groups, h, c)
+    assert explain.graph_break_count == 0
+    assert torch.equal(compiled, per_module)

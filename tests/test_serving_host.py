@@ -44,3 +44,20 @@ def test_wrap_bank_structure_and_assign(fuse):
     assert all(m.assign is assign for m in wrapped.values())
     lead = model.single_transformer_blocks[1].attn.to_q
     assert (lead.layer if fuse else lead).assign is assign
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_stage_groups_structure(fuse):
+    """stage_groups: per double block the proj (6), out (2), up (2) and down (2) stages, per single
+    block its q / k / v, members in call order (shared-input stand-ins resolved to their layers)."""
+    model = ToyFlux(n_double=2, n_single=3)
+    wrapped = serving.wrap_bank(model, _bank(model), fuse_shared_inputs=fuse)
+    groups = serving.stage_groups(wrapped)
+    assert len(groups) == 2 * 4 + 3
+    g = groups[("transformer_blocks.1.", "proj")]
+    names = ["attn.to_q", "attn.to_k", "attn.to_v", "attn.add_q_proj", "attn.add_k_proj", "attn.add_v_proj"]
+    assert [l.base for l in g.layers] == [getattr(wrapped["transformer_blocks.1." + n], "base") for n in names]
+    assert len(groups[("single_transformer_blocks.2.", "proj")].layers) == 3
+    assert len(groups[("transformer_blocks.0.", "down")].layers) == 2
+    with pytest.raises(ValueError):
+        serving.StageGroup([])
