@@ -248,6 +248,105 @@ __global__ void __launch_bounds__(kThreads) decode_packed3_kernel(DecodeArgs a) 
     }
 }
 
+// Packed 3-level bulk decode to bf16, software-pipelined, whole-line stores. Each thread runs
+// kLineBatches batches of kLineBatch half-blocks (spaced kThreads apart, consecutive threads on
+// consecutive half-blocks); the index loads of batch i + 1 are in flight while batch i is decoded
+// and stored. Per half-block a lane decodes its 8 distinct values once; the wave's 64 halves
+// (32 blocks) go through a 1 KB LDS exchange and every store instruction writes 8 whole 128-byte
+// lines: lane L stores chunk L % 8 (half (L % 8) & 1 of the period) of block 8 s + L / 8.
+// Measured on MI355X (FLUX 342-linear layout, 2,000-slot bank): 5.48 TB/s at rank 16 and 5.43 at
+// rank 64, against 4.83 / 4.62 for decode_packed3_kernel (24 half-blocks per thread, all loads
+// before the first store, each lane storing its 8 values 4 times at a 32-byte stride). The same
+// pipeline with that store shape ran 3.99 / 3.94; non-temporal line stores 5.36 / 5.37; 4 or 16
+// half-blocks per batch, 1, 4 or 8 batches per workgroup 5.05-5.40 (8 x 4 and wider spill or drop
+// to 3 waves per SIMD). Stacked output (decoded-mode serving): a lane finds the output block of
+// the block it stores, walking the segment table forward.
+constexpr int kLineBatch = 8;
+constexpr int kLineBatches = 2;
+__global__ void __launch_bounds__(kThreads) decode_packed3_lines_kernel(DecodeArgs a) {
+    constexpr int B = kLineBatch;
+    constexpr int PER_WG = kThreads * B * kLineBatches;    // half-blocks per workgroup
+    constexpr int SPAN = PER_WG / 2;                       // blocks per workgroup
+    static_assert(SPAN % (4 * kThreads) == 0, "whole 4-byte side loads per thread");
+    __shared__ float lut[2 * kMaxLevels * 10];
+    __shared__ int8_t wg_side[SPAN];
+    __shared__ bf16x8 xch[kThreads];                       // 1 KB per wave
+    if (threadIdx.x < 2 * kMaxLevels * 10) lut[threadIdx.x] = (&a.luts.v[0][0][0])[threadIdx.x];
+    const int64_t b0 = (int64_t)blockIdx.x * SPAN;
+    const bool whole = a.sides && b0 + SPAN <= a.n_blocks && (reinterpret_cast<uintptr_t>(a.sides) & 3u) == 0;
+    const int sel = blockIdx.y;
+    const int64_t slot = a.slots ? a.slots[sel] : 0;
+    const bool bad = slot < 0 || slot >= a.src.n_slots;
+    const int64_t halves = a.n_blocks * 2;
+    const int lane = threadIdx.x & 63;
+    const int64_t h0 = (int64_t)blockIdx.x * PER_WG + threadIdx.x;
+    __bf16 *out = static_cast<__bf16 *>(a.out) + (a.seg ? 0 : (int64_t)sel * a.out_sel_stride);
+    int32_t sg = a.seg ? find_seg(a, std::min(b0, a.n_blocks - 1)) : 0;
+
+    RawIdx raw[2][B];
+    auto loads = [&](int i, RawIdx *r) __attribute__((always_inline)) {
+        int64_t sl[B], blk[B];
+#pragma unroll
+        for (int q = 0; q < B; ++q) {
+            blk[q] = std::min(h0 + (int64_t)(i * B + q) * kThreads, halves - 1) >> 1;   // clamped: in range
+            sl[q] = bad ? 0 : slot;
+        }
+        load_raw<B, true, 3>(a.src, sl, blk, r);
+    };
+    loads(0, raw[0]);
+    if (whole) {
+        uint32_t sw[SPAN / (4 * kThreads)];
+#pragma unroll
+        for (int q = 0; q < SPAN / (4 * kThreads); ++q)
+            sw[q] = *reinterpret_cast<const uint32_t *>(a.sides + b0 + 4 * (int64_t)(threadIdx.x + q * kThreads));
+#pragma unroll
+        for (int q = 0; q < SPAN / (4 * kThreads); ++q)
+            *reinterpret_cast<uint32_t *>(wg_side + 4 * (threadIdx.x + q * kThreads)) = sw[q];
+    }
+    __syncthreads();    // value tables (and staged sides) visible
+    if (bad && threadIdx.x == 0 && blockIdx.x == 0) record_error(a.err, kErrSlot);
+
+    bf16x8 *wx = xch + (threadIdx.x & ~63);
+#pragma unroll
+    for (int i = 0; i < kLineBatches; ++i) {
+        if (i + 1 < kLineBatches) loads(i + 1, raw[(i + 1) & 1]);
+#pragma unroll
+        for (int q = 0; q < B; ++q) {
+            const int64_t hf = h0 + (int64_t)(i * B + q) * kThreads;
+            const int64_t blk = std::min(hf, halves - 1) >> 1;
+            const int h = (int)(hf & 1);
+            uint32_t k[kMaxLevels];
+            extract_indices<true, 3>(a.src, blk, raw[i & 1][q], k);
+            const int sd = whole ? wg_side[blk - b0] : (a.sides ? a.sides[blk] : 0);
+            const float *tab = lut + sd * kMaxLevels * 10;
+            bf16x8 pk;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t m = h ? sign_mask(8 + e) : sign_mask(e);
+                pk[e] = (__bf16)(bad ? 0.0f : decode_value<3>(tab, 3, k, m));
+            }
+            // the wave's lanes hold halves hw .. hw + 63 (hw even) = blocks hw / 2 .. hw / 2 + 31
+            wave_lds_sync();     // the other lanes have read the previous halves
+            xch[threadIdx.x] = pk;
+            wave_lds_sync();     // every lane's half is in the exchange
+            const int64_t bw = (hf - lane) >> 1;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int mb = 8 * st + (lane >> 3), c = lane & 7;
+                const bf16x8 v = wx[2 * mb + (c & 1)];
+                const int64_t b = bw + mb;
+                if (b >= a.n_blocks) continue;
+                const int64_t ob = a.seg ? stacked_block(a, sg, b, sel) : b;
+                if (a.seg && (ob < 0 || ob >= (int64_t)a.n_sel * a.n_blocks)) {    // table inconsistent with n_blocks
+                    record_error(a.err, kErrTable);
+                    continue;
+                }
+                *reinterpret_cast<bf16x8 *>(out + ob * kBlock + 8 * c) = v;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 // True when blocks [block_off, block_off + n_blocks) of every slot lie inside the slot's
@@ -365,6 +464,12 @@ static int32_t decode_impl(const lithe_index_src *src, const int32_t *slots, int
     const int64_t halves = n_blocks * 2;
     // the widest grid is the one-half-block-per-thread kernel's
     if ((halves + kThreads - 1) / kThreads > kMaxGridX || n_sel > kMaxGridY) return LITHE_ERR_SHAPE;
+    if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3 && out_dtype == LITHE_DT_BF16) {
+        constexpr int64_t per_wg = (int64_t)kThreads * kLineBatch * kLineBatches;
+        dim3 grid((unsigned)((halves + per_wg - 1) / per_wg), (unsigned)n_sel);
+        hipLaunchKernelGGL(decode_packed3_lines_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+        return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+    }
     if (src->kind == LITHE_IDX_PACKED9 && src->num_levels == 3) {
         const int64_t per_wg = (int64_t)kThreads * kDecodeIter;
         dim3 grid((unsigned)((halves + per_wg - 1) / per_wg), (unsigned)n_sel);

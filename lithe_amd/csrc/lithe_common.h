@@ -186,6 +186,16 @@ template <> struct DT<float> {
     __device__ static __forceinline__ float round(float f) { return f; }
 };
 
+// Orders the LDS accesses of one wave around a cross-lane exchange: every access before it (in
+// program order) is complete and visible to the other lanes of the wave before any access after
+// it. The LDS executes one wave's accesses in order, so this costs no wait; it keeps the compiler
+// from moving a lane's accesses across the exchange point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ void record_error(int32_t *err, int32_t bits) {
     if (err) __hip_atomic_fetch_or(err, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -206,16 +206,6 @@ __device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
     }
 }
 
-// Orders the LDS accesses of one wave around a cross-lane exchange: every access before it (in
-// program order) is complete and visible to the other lanes of the wave before any access after
-// it. The LDS executes one wave's accesses in order, so this costs no wait; it keeps the compiler
-// from moving a lane's accesses across the exchange point.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // ============================================================================ shrink
 // Workgroup = 4 waves of one sample; each wave owns 16 tokens and 1/ks of every K piece
 // (ks waves share a token group). K is cut into pieces of pb blocks, and the sample's A
