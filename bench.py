@@ -14,7 +14,7 @@ attention outputs, the two up and the two down projections, a single block's
 q / k / v) run as one grouped call: one shrink and one expand launch per stage,
 114 calls per sweep (``--config flux342``: one call per module).
 
-    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|ffn|hb|decode|ingest|encode] [--rank 16|64]
+    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|ffn|hb|hb_modules|decode|ingest|encode] [--rank 16|64]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -685,8 +685,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="grouped",
-                    choices=["flux342", "qkv", "grouped", "fused", "decoded", "ffn", "hb", "decode", "ingest",
-                             "encode"])
+                    choices=["grouped", "flux342", "fused", "qkv", "decoded", "ffn", "hb", "hb_modules", "decode",
+                             "ingest", "encode"])
     ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -731,15 +731,17 @@ def main():
                          "attention outputs, up and down projections) in one shrink + one expand launch")
         if args.config != "flux342":
             workload += f" ({len(wl.calls)} calls per sweep)"
-    elif args.config == "hb":
+    elif args.config in ("hb", "hb_modules"):
         mods, batch, n_slots = flux_modules(256, 512), 96, args.slots or 10_000
         ranks = np.arange(1, n_slots + 1, dtype=np.float64)
         p = ranks ** -1.1
         p /= p.sum()
         perm = rng.permutation(n_slots)
         assign = perm[rng.choice(n_slots, batch, p=p)]
-        wl = Workload("hb", mods, batch, n_slots, assign)
+        wl = Workload("hb", mods, batch, n_slots, assign, grouped=args.config == "hb")
         workload = "FLUX.1-dev 342 linears, 256^2: B=96 x 768 tokens (256 img + 512 txt), Zipf(1.1) over 10k bank"
+        workload += (", grouped: one shrink + one expand launch per block stage" if args.config == "hb"
+                     else ", one call per module") + f" ({len(wl.calls)} calls per sweep)"
     else:
         full = flux_modules(1024, 512)
         mods = [("transformer_blocks.0.ff.net.0.proj", 3072, 12288, 1536),
@@ -768,7 +770,7 @@ def main():
         _, di, do, m = group[0]
         if len(group) == 1:
             k = f"{di}->{do} x {m}"
-        elif args.config in ("grouped", "fused"):
+        elif args.config in ("grouped", "fused", "hb"):
             k = "group " + " + ".join(sorted({f"{g[1]}->{g[2]} x {g[3]}" for g in group}))
         else:
             k = f"{di}->{len(group)}x{do} x {m} (shared x)"
@@ -809,7 +811,9 @@ def main():
         "roofline": {"kernel": {"qkv": "lithe_lora_delta / lithe_lora_delta_shared_x (one shrink + one expand per module)",
                                 "grouped": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)",
                                 "fused": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage, "
-                                         "q/k/v sharing x)"}.get(args.config,
+                                         "q/k/v sharing x)",
+                                "hb": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)"}.get(
+                                    args.config,
                                                                  "lithe_lora_delta (shrink + expand, one call per module)"),
                      "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

@@ -112,6 +112,7 @@ struct LoraArgs {
 // Launch plan of one call (host side; the kernels read the fields copied into LoraArgs).
 struct Plan {
     int G, n_rg, GM, MR;
+    int GMs;    // rank groups the shrink is compiled for (GM, or exactly 3 for three groups)
     int tiles_s, ks, pb, arow, region, red_off, stage_off;
     size_t lds_s, lds_e;
     int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off;
@@ -218,9 +219,12 @@ __device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
 // XNT: x loads carry the non-temporal hint (x is read once). The replicated shared-input form
 // reads each x line from several workgroups of one XCD and keeps it in L2 instead.
 // bid: the workgroup's index within this call's grid (a grouped launch passes it relative to the
-// call's first workgroup); ids past the call's tiles (padding) return at once.
+// call's first workgroup); ids past the call's tiles (padding) return at once. goff: the first A
+// block of each group (kMaxGroups entries in kernel-argument memory; a grouped launch passes its
+// job's table, so its local copy of the arguments is only read at constant offsets and stays in
+// registers).
 template <typename XT, int SRC, int GM, int U, bool XNT>
-__device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid) {
+__device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const int64_t *goff) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     constexpr bool kBf16 = sizeof(XT) == 2;
     constexpr int KSTEP = kBf16 ? 32 : 16;
@@ -287,14 +291,14 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid) {
         return r;
     };
     // module of this workgroup's A in replicated mode (uniform), a_goff[mod]
-    int64_t mod_aoff = a.a_goff[0];
+    int64_t mod_aoff = goff[0];
 #pragma unroll
-    for (int q = 1; q < kMaxGroups; ++q) mod_aoff = mod == q ? a.a_goff[q] : mod_aoff;
+    for (int q = 1; q < kMaxGroups; ++q) mod_aoff = mod == q ? goff[q] : mod_aoff;
     auto group_aoff = [&](int g) __attribute__((always_inline)) -> int64_t {   // a_goff[g], branch-free
         if (a.n_mod_wg > 1) return mod_aoff;
-        int64_t r = a.a_goff[0];
+        int64_t r = goff[0];
 #pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? a.a_goff[q] : r;
+        for (int q = 1; q < GM; ++q) r = g == q ? goff[q] : r;
         return r;
     };
     if constexpr (SRC != SRC_DENSE) stage_lut(lut, a.luts.v[0][0], tid);
@@ -308,10 +312,9 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid) {
     // most kFillBatch items per thread (the plan keeps GM * 16 * pb <= kFillBatch * kThreads);
     // the index loads of a piece are issued one piece ahead of its decode.
     // item it of a piece: row gr = it % (GM*16), block c = it / (GM*16) (block-major: a shift)
-    constexpr int kRowsLog2 = GM == 1 ? 4 : GM == 2 ? 5 : GM == 4 ? 6 : 7;
     auto idx_item = [&](int g, int it, int &gr, int &c, bool &live) __attribute__((always_inline)) -> int64_t {
-        gr = it & (GM * 16 - 1);
-        c = it >> kRowsLog2;
+        gr = it % (GM * 16);     // constant divisor: a mask and a shift for power-of-two GM
+        c = it / (GM * 16);
         const int grp = gr >> 4;
         const int rr = group_rank0(grp) + (gr & 15);
         live = group_slot(grp) >= 0 && rr < a.rank;
@@ -605,7 +608,7 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid) {
 
 template <typename XT, int SRC, int GM, int U, bool XNT>
 __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
-    shrink_body<XT, SRC, GM, U, XNT>(a, (int)blockIdx.x);
+    shrink_body<XT, SRC, GM, U, XNT>(a, (int)blockIdx.x, a.a_goff);
 }
 
 // ============================================================================ expand
@@ -1081,8 +1084,6 @@ __host__ __device__ __forceinline__ void apply_job(LoraArgs &a, const GroupJob &
     a.d_in = j.d_in;
     a.d_out = j.d_out;
     a.rows = j.rows;
-#pragma unroll
-    for (int q = 0; q < kMaxGroups; ++q) a.a_goff[q] = j.a_goff[q];
     a.b_src.block_off = j.b_off;
     a.MR = j.MR;
     a.mid_goff = j.mid_goff;
@@ -1111,8 +1112,8 @@ __global__ void __launch_bounds__(kThreads) shrink_group_kernel(GroupArgs g) {
     const int j = group_job(g, bid);
     LoraArgs a = g.a;
     apply_job(a, g.job[j]);
-    if (g.job[j].xnt) shrink_body<XT, SRC, GM, U, true>(a, bid - g.begin[j]);
-    else shrink_body<XT, SRC, GM, U, false>(a, bid - g.begin[j]);
+    if (g.job[j].xnt) shrink_body<XT, SRC, GM, U, true>(a, bid - g.begin[j], g.job[j].a_goff);
+    else shrink_body<XT, SRC, GM, U, false>(a, bid - g.begin[j], g.job[j].a_goff);
 }
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
@@ -1164,6 +1165,7 @@ void dispatch_shrink_group(int GM, const GroupArgs &g, unsigned grid, size_t lds
     switch (GM) {
         case 1: launch_shrink_group<XT, SRC, 1>(g, grid, lds, st); break;
         case 2: launch_shrink_group<XT, SRC, 2>(g, grid, lds, st); break;
+        case 3: launch_shrink_group<XT, SRC, 3>(g, grid, lds, st); break;
         case 4: launch_shrink_group<XT, SRC, 4>(g, grid, lds, st); break;
         default: launch_shrink_group<XT, SRC, 8>(g, grid, lds, st); break;
     }
@@ -1185,9 +1187,10 @@ void dispatch_expand_group(int GM, int BOM, const GroupArgs &g, unsigned grid, s
 
 template <typename XT, int SRC>
 void dispatch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    switch (p.GM) {
+    switch (p.GMs) {
         case 1: launch_shrink<XT, SRC, 1>(p, a, st); break;
         case 2: launch_shrink<XT, SRC, 2>(p, a, st); break;
+        case 3: launch_shrink<XT, SRC, 3>(p, a, st); break;
         case 4: launch_shrink<XT, SRC, 4>(p, a, st); break;
         default: launch_shrink<XT, SRC, 8>(p, a, st); break;
     }
