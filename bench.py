@@ -467,7 +467,7 @@ def run_decode(args):
                    "rank": rank, "bank_slots": n_slots, "bank_GB": round(n_slots * in_per / 1e9, 2),
                    "adapters_per_launch": chunk, "out_MB_per_adapter": round(out_per / 1e6, 2)},
         "adapters_per_s": round(n_slots / (ms * 1e-3), 1),
-        "roofline": {"kernel": "decode_kernel (lithe_decode)", "bound": "hbm", "achieved": round(achieved, 1),
+        "roofline": {"kernel": "decode_packed3_lines_kernel (lithe_decode)", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": launch_bytes,
                      "mean_launch_ms": round(launch_ms, 4)},
