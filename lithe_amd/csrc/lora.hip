@@ -110,12 +110,29 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
     // 2 sub-tiles of 64 tokens per workgroup only for mid-sized grids (the 512-token, 3072-output
     // FLUX modules); everywhere else one sub-tile (more, shorter workgroups) measured faster.
-    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !narrow && !ctx) ? 2 : 1;
+    // Waves along the outputs of a workgroup (2^wo_sh of them, BO outputs each; the others along
+    // the tokens): a workgroup's y tile is 64 / 2^wo_sh token rows x 2^wo_sh * BO outputs. bf16 y
+    // takes two: read-modify-write probes (1 GB of 6 KB / 24 KB rows) moved 64-row x 256 B tiles
+    // at 5.53 / 5.60 TB/s, 32 x 256 B at 5.79 / 6.07, 64 x 512 B at 5.78 / 5.82, 32 x 1 KB at
+    // 5.95-6.09 / 6.26-6.42, 2 KB-wide tiles at 5.5-5.8. On the grouped FLUX sweep: 57.7 -> 55.4 ms
+    // (128-output waves 4 along the outputs, 16 x 1 KB tiles: 55.9 ms; 128-output waves 1 along the
+    // outputs: 55.6 ms).
+    int wo = ybytes == 2 && !dense ? 2 : 1;
+    if (getenv("LITHE_EXPAND_WO")) {
+        const int v = env_int("LITHE_EXPAND_WO", 1);
+        wo = v >= 4 ? 4 : v >= 2 ? 2 : 1;
+    }
+    if (dense) wo = 1;
+    while (wo > 1 && (int64_t)wo * p.BO > ((d_out + 31) / 32) * 32) wo >>= 1;
+    p.wo_sh = wo == 4 ? 2 : wo == 2 ? 1 : 0;
+    // (with several waves along the outputs one sub-tile measured faster on every FLUX sweep)
+    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !narrow && !ctx && wo == 1) ? 2 : 1;
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
-    p.tiles_e = (int)std::max<int64_t>(1, (seq + 64 * (int64_t)subs - 1) / (64 * (int64_t)subs));
-    // B periods of one output tile: the blocks covering outputs [obase, obase + BO) of a route
-    p.nblk_max = (int)(((int64_t)p.BO * rank + kBlock - 1) / kBlock + 1);
+    const int64_t tps = 64 / wo;     // tokens per sub-tile
+    p.tiles_e = (int)std::max<int64_t>(1, (seq + tps * subs - 1) / (tps * subs));
+    // B periods of one workgroup's outputs: the blocks covering [obase, obase + wo * BO) of a route
+    p.nblk_max = (int)(((int64_t)wo * p.BO * rank + kBlock - 1) / kBlock + 1);
     p.lds_e = kHead + (dense ? (size_t)n_route * p.BO * rank * xbytes : (size_t)n_route * p.nblk_max * 16 * xbytes);
     // whole-line y path (bf16 y, output tiles of whole lines): a 16 x BOM bf16 tile per wave
     p.estage_off = (int)((p.lds_e + 15) & ~size_t(15));
@@ -175,6 +192,7 @@ void set_expand_fields(LoraArgs &a, const Plan &p) {
     a.BO = p.BO;
     a.nblk_max = p.nblk_max;
     a.estage_off = p.estage_off;
+    a.wo_sh = p.wo_sh;
 }
 
 }  // namespace
@@ -232,7 +250,8 @@ int32_t check_indexed(const lithe_factors *f, int32_t rank, int64_t d_in, int64_
 // XCD rounds) and of the expand (bounded over its sub-tile choices) fit a launch.
 bool grids_fit(const Plan &p, int64_t n_batch, int64_t d_out, int n_mod_wg) {
     const int64_t shrink = n_mod_wg > 1 ? (n_batch * p.tiles_s + 7) / 8 * 8 * n_mod_wg : n_batch * p.tiles_s;
-    const int64_t expand = ((d_out + p.BO - 1) / p.BO) * n_batch * p.tiles_e * p.subs_e;
+    const int64_t bow = (int64_t)p.BO << p.wo_sh;
+    const int64_t expand = ((d_out + bow - 1) / bow) * n_batch * p.tiles_e * p.subs_e;
     return shrink <= kMaxGridX && expand <= kMaxGridX;
 }
 
@@ -641,9 +660,11 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
         j.vec_y = (md.d_out % 8 == 0) && (((uintptr_t)md.y & 15u) == 0);
         j.nblk_max = p.nblk_max;
         j.estage_off = p.estage_off;
+        j.wo_sh = p.wo_sh;
         j.out_scale = md.out_scale;
         ge.begin[k] = (int32_t)wg;
-        wg += round8(((md.d_out + p.BO - 1) / p.BO) * n_batch * p.tiles_e);
+        const int64_t bow = (int64_t)p.BO << p.wo_sh;
+        wg += round8(((md.d_out + bow - 1) / bow) * n_batch * p.tiles_e);
         lds_e = std::max(lds_e, p.lds_e);
     }
     ge.n_jobs = n_act;

@@ -68,7 +68,12 @@ static_assert(kShrinkU % kStageLoads == 0 && kStageLoads % 2 == 0, "the stage ta
 #ifndef LITHE_EXCHANGE_OUTPUTS
 #define LITHE_EXCHANGE_OUTPUTS 128
 #endif
+#ifndef LITHE_LINE_UNITS
+#define LITHE_LINE_UNITS 8     // 16-byte units of one token row per whole-line y access (8, 16, 32)
+#endif
 constexpr int kExchangeOutputs = LITHE_EXCHANGE_OUTPUTS;   // outputs per expand LDS exchange (whole-line y)
+constexpr int kLineUnits = LITHE_LINE_UNITS;
+static_assert(kLineUnits == 8 || kLineUnits == 16 || kLineUnits == 32, "a y access covers 8, 4 or 2 token rows");
 
 // Factor sources: SRC_PACKED is SRC_INDEXED with both index streams PACKED9 with 3 levels (the
 // resident bank of the twin codebook), compiled without the kind dispatch of the other index
@@ -86,6 +91,7 @@ struct LoraArgs {
     int32_t rank, G, n_rg, n_route, MR;
     int32_t tiles_s, ks, pb, arow, region, red_off, stage_off;
     int32_t tiles_e, subs_e, BO, vec_y, nblk_max, estage_off;
+    int32_t wo_sh;      // expand: 2^wo_sh waves along the outputs of a workgroup (BO outputs each)
     int32_t accumulate;
     float out_scale;
     const int32_t *r_slot;
@@ -115,7 +121,7 @@ struct Plan {
     int GMs;    // rank groups the shrink is compiled for (GM, or exactly 3 for three groups)
     int tiles_s, ks, pb, arow, region, red_off, stage_off;
     size_t lds_s, lds_e;
-    int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off;
+    int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off, wo_sh;
     int64_t off_mid, total;
 };
 
@@ -133,7 +139,7 @@ struct GroupJob {
     int64_t b_off;
     int32_t MR, mid_goff, n_mod_wg, xnt;
     int32_t tiles_s, ks, pb, arow, region, red_off, stage_off;
-    int32_t tiles_e, subs_e, BO, vec_y, nblk_max, estage_off;
+    int32_t tiles_e, subs_e, BO, vec_y, nblk_max, estage_off, wo_sh;
     float out_scale;
 };
 struct GroupArgs {
@@ -656,8 +662,14 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
-    const int o_tiles = (int)((a.d_out + a.BO - 1) / a.BO);
-    const int64_t obase = (int64_t)(bid % o_tiles) * a.BO;
+    // Workgroup tile: 2^wo_sh waves along the outputs (BO each) x 4 / 2^wo_sh waves along the
+    // tokens (16 each per sub-tile); wave (wt, wq) takes tokens wt * 16 .. and outputs obase ..
+    const int wt = wave >> a.wo_sh, wq = wave & ((1 << a.wo_sh) - 1);
+    const int BOW = a.BO << a.wo_sh;                   // outputs per workgroup
+    const int TPS = (kWaves >> a.wo_sh) * 16;          // tokens per sub-tile
+    const int o_tiles = (int)((a.d_out + BOW - 1) / BOW);
+    const int64_t obase_wg = (int64_t)(bid % o_tiles) * BOW;
+    const int64_t obase = obase_wg + (int64_t)wq * a.BO;
     const int tile = bid / o_tiles;
     if (tile >= (int)a.n_batch * a.tiles_e) return;    // padding of a grouped call (before any barrier)
     const int64_t b = tile / a.tiles_e;
@@ -672,7 +684,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
         any = any || gslot[g] >= 0;
     }
     auto sub_row = [&](int sub, bool &valid) __attribute__((always_inline)) -> int64_t {
-        const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + r16;
+        const int64_t m = ((int64_t)mt * a.subs_e + sub) * TPS + wt * 16 + r16;
         valid = m < a.seq;
         return b * a.seq + (valid ? m : a.seq - 1);
     };
@@ -693,31 +705,35 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     constexpr int NP = BOM / 32;
     const int np = a.BO / 32;
 
-    // Whole-line y path (bf16 y): rows of this wave's two 8-token halves of sub-tile `sub`, and
-    // its y loads (access j: token 8 (j & 1) + lane / 8, outputs 64 (j >> 1) + 8 (lane % 8) ..).
+    // Whole-line y path (bf16 y): access j of a wave's 16 x BOM tile covers token rows
+    // IR (j % RB) + lane / IC and 16-byte units IC (j / RB) + lane % IC (IC units of IR rows, whole
+    // 128-byte lines); lrow holds the rows of the RB row blocks of sub-tile `sub`.
     // They are issued per sub-tile, after the B tile is built. Issued earlier they cost the
     // sweep 1.8 % ahead of the B index loads (the decode waits behind them: loads complete in
     // order) and 2.6 % right behind them (the decode does not wait, but the tile's y registers
     // stay live through the decode and the barrier).
     constexpr int NJ = BOM / 32;
+    constexpr int HB = kExchangeOutputs < BOM ? kExchangeOutputs : BOM;   // outputs per exchange
+    constexpr int IC = kLineUnits < HB / 8 ? kLineUnits : HB / 8;
+    constexpr int IR = 64 / IC, RB = 16 / IR;
     const int64_t omax = a.d_out - 8;
     auto line_rows = [&](int sub, int64_t *lrow, bool *lval) __attribute__((always_inline)) {
 #pragma unroll
-        for (int eta = 0; eta < 2; ++eta) {
-            const int64_t m = ((int64_t)mt * a.subs_e + sub) * (kWaves * 16) + wave * 16 + 8 * eta + (lane >> 3);
-            lval[eta] = m < a.seq;
-            lrow[eta] = (b * a.seq + (lval[eta] ? m : a.seq - 1)) * a.d_out;
+        for (int rb = 0; rb < RB; ++rb) {
+            const int64_t m = ((int64_t)mt * a.subs_e + sub) * TPS + wt * 16 + IR * rb + lane / IC;
+            lval[rb] = m < a.seq;
+            lrow[rb] = (b * a.seq + (lval[rb] ? m : a.seq - 1)) * a.d_out;
         }
     };
     auto line_load = [&](int sub, bf16x8 *yv) __attribute__((always_inline)) {
-        int64_t lrow[2];
-        bool lval[2];
+        int64_t lrow[RB];
+        bool lval[RB];
         line_rows(sub, lrow, lval);
         const __bf16 *yb = static_cast<const __bf16 *>(a.y);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
             yv[j] = stream_load<bf16x8, true>(reinterpret_cast<const bf16x8 *>(
-                yb + lrow[j & 1] + std::min<int64_t>(obase + 64 * (j >> 1) + 8 * (lane & 7), omax)));
+                yb + lrow[j % RB] + std::min<int64_t>(obase + 8 * (IC * (j / RB) + lane % IC), omax)));
     };
 
     // mid fragments; groups without an adapter read group 0 of the same row (their B
@@ -751,13 +767,15 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     // ---- B tile of this output range into LDS (bp), read from there by every MFMA.
     // Indexed: the 16-value periods of blocks [blk_lo, blk_lo + nblk) of every route entry,
     // one item per quarter period (4 values), 2 items per thread per batch.
-    // Dense: rows o in [obase, o_end) of every route entry's B, (route, o - obase, rank).
+    // Dense: rows o in [obase_wg, o_end_wg) of every route entry's B, (route, o - obase_wg, rank).
     float *lut = reinterpret_cast<float *>(smem);
     XT *bp = reinterpret_cast<XT *>(smem + kHead);
-    const int64_t blk_lo = (obase * a.rank) >> 6;
+    // the tile covers the workgroup's outputs [obase_wg, o_end_wg); o_end bounds this wave's
+    const int64_t blk_lo = (obase_wg * a.rank) >> 6;
+    const int64_t o_end_wg = std::min<int64_t>(obase_wg + BOW, a.d_out);
     const int64_t o_end = std::min<int64_t>(obase + a.BO, a.d_out);
     if constexpr (SRC != SRC_DENSE) {
-        const int per_route = (int)(((o_end * a.rank + kBlock - 1) >> 6) - blk_lo) * 4;
+        const int per_route = (int)(((o_end_wg * a.rank + kBlock - 1) >> 6) - blk_lo) * 4;
         const int items = a.n_route * per_route;
         RawIdx raw[2];
         // block of item `it` inside the factor; 0 if its route entry is empty
@@ -817,9 +835,9 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             dec_store(base);
         }
     } else {
-        // 16-byte vectors of (o_end - obase) * rank consecutive values per route entry
+        // 16-byte vectors of (o_end_wg - obase_wg) * rank consecutive values per route entry
         constexpr int EV = 16 / sizeof(XT);
-        const int per_route = (int)((o_end - obase) * a.rank / EV);
+        const int per_route = (int)((o_end_wg - obase_wg) * a.rank / EV);
         const int items = a.n_route * per_route;
         for (int it = tid; it < items; it += kThreads) {
             const int j = it / per_route, c = it - j * per_route;
@@ -829,8 +847,8 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             if (slot >= 0)
                 v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_b) +
-                                                     (slot * a.d_out + obase) * a.rank + (int64_t)c * EV);
-            *reinterpret_cast<f32x4 *>(bp + (int64_t)j * a.BO * a.rank + (int64_t)c * EV) = v;
+                                                     (slot * a.d_out + obase_wg) * a.rank + (int64_t)c * EV);
+            *reinterpret_cast<f32x4 *>(bp + (int64_t)j * BOW * a.rank + (int64_t)c * EV) = v;
         }
     }
     __syncthreads();
@@ -844,7 +862,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             const int64_t f = o * a.rank + r;
             return ((int64_t)j * a.nblk_max + (f >> 6) - blk_lo) * 16 + (f & 15);
         } else {
-            return ((int64_t)j * a.BO + (o - obase)) * a.rank + r;
+            return ((int64_t)j * BOW + (o - obase_wg)) * a.rank + r;
         }
     };
     auto bfrag = [&](int p, int h, int g) __attribute__((always_inline)) -> Frag {
@@ -903,16 +921,16 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     // (rows and columns clamped in range); waves of other workgroups hide the latency.
 
     // Whole-line y path (bf16 y). The y tile of a wave (16 tokens x BOM outputs) moves in
-    // loads and stores that each cover whole 128-byte lines: access j gives lane L token
-    // 8 (j & 1) + L / 8 and outputs 64 (j >> 1) + 8 (L % 8) .. + 7, with the non-temporal hint
-    // (measured: +5 % read-modify-write bandwidth; split-line accesses lose with it). The
+    // loads and stores that each cover whole 128-byte lines (default: 8 token rows x 128 B per
+    // access; 4 x 256 B and 2 x 512 B measured 0.3-0.5 % slower on the grouped FLUX sweep), with
+    // the non-temporal hint (measured: +5 % read-modify-write bandwidth; split-line accesses lose
+    // with it). The
     // delta d = round_y(round_y(acc) * s) is finished in the MFMA layout (lane: token r16,
     // outputs 32 p + 8 gq ..) and exchanged through a per-wave LDS tile, HB outputs at a time
     // (a 4 KB tile: the workgroup's LDS stays small enough for 8 workgroups per CU): 16-byte
     // unit (token t, chunk q) at (HB / 8) t + (q ^ swz(t)), conflict-free for both sides at
     // HB >= 128. A wave reuses its tile for the next half after reading it back (LDS accesses
     // of one wave complete in order).
-    constexpr int HB = kExchangeOutputs < BOM ? kExchangeOutputs : BOM;   // outputs per exchange
     auto line_subtile = [&](int sub, const Frag *mf, const bf16x8 *yv) __attribute__((always_inline)) {
         __bf16 *stg = reinterpret_cast<__bf16 *>(smem + a.estage_off) + wave * 16 * HB;
         constexpr int RU = HB / 8;     // 16-byte units per token row of the tile
@@ -920,9 +938,8 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             const int swz = ((t & 7) | ((((t >> 3) ^ t) & 1) << 3)) & (RU - 1);
             return stg + (RU * t + (q ^ swz)) * 8;
         };
-        const int lr = lane >> 3, lc = lane & 7;
-        int64_t lrow[2];
-        bool lval[2];
+        int64_t lrow[RB];
+        bool lval[RB];
         line_rows(sub, lrow, lval);
         __bf16 *yb = static_cast<__bf16 *>(a.y);
         constexpr int PH = HB / 32;    // MFMA column groups (and y accesses) per exchange
@@ -942,7 +959,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             wave_lds_sync();    // every lane's deltas are in the tile before any lane reads them
 #pragma unroll
             for (int j = h * PH; j < (h + 1) * PH; ++j) {
-                const int t = 8 * (j & 1) + lr, q = 8 * (j >> 1) + lc;
+                const int t = IR * (j % RB) + lane / IC, q = IC * (j / RB) + lane % IC;
                 const bf16x8 d = *reinterpret_cast<const bf16x8 *>(unit(t, q - h * RU));
                 const int64_t o8 = obase + 8 * q;
                 bf16x8 out;
@@ -952,8 +969,8 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
                 } else {
                     out = d;
                 }
-                if (lval[j & 1] && 8 * q < a.BO && o8 < a.d_out)
-                    stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + lrow[j & 1] + o8), out);
+                if (lval[j % RB] && 8 * q < a.BO && o8 < a.d_out)
+                    stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + lrow[j % RB] + o8), out);
             }
         }
     };
@@ -1048,7 +1065,8 @@ void launch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
 
 template <typename XT, typename YT, int SRC, int GM, int BOM>
 void launch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
-    dim3 ge((unsigned)(((a.d_out + p.BO - 1) / p.BO) * a.n_batch * p.tiles_e));
+    const int64_t bow = (int64_t)p.BO << p.wo_sh;
+    dim3 ge((unsigned)(((a.d_out + bow - 1) / bow) * a.n_batch * p.tiles_e));
     const bool quad = (a.rank & 3) == 0;
     if constexpr (GM == 1 && sizeof(YT) == 2) {
         if (quad) {
@@ -1101,6 +1119,7 @@ __host__ __device__ __forceinline__ void apply_job(LoraArgs &a, const GroupJob &
     a.vec_y = j.vec_y;
     a.nblk_max = j.nblk_max;
     a.estage_off = j.estage_off;
+    a.wo_sh = j.wo_sh;
     a.out_scale = j.out_scale;
 }
 

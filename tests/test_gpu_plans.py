@@ -1,12 +1,12 @@
 """GPU parity of the delta's launch plans and output paths that the serving shapes reach only at
 sizes too large for the oracle, on small shapes with the plan forced through the plan overrides
-(LITHE_SHRINK_KS, LITHE_EXPAND_BO, LITHE_EXPAND_SUBS; the library reads them on every call):
+(LITHE_SHRINK_KS, LITHE_EXPAND_BO, LITHE_EXPAND_WO, LITHE_EXPAND_SUBS; the library reads them on every call):
 
 * the shrink with each token group's K range on 1, 2 or 4 waves (one rank group): 2 waves is the
   plan of the 12288 -> 3072 projections at 1,536 and 4,096 tokens. Results differ only in the fp32
   grouping of the K sum, so each is checked against the oracle;
-* the expand with 128- and 256-output tiles and 1 or 2 sub-tiles per workgroup: the same sums in
-  the same order, so the outputs are bit-identical to each other;
+* the expand with 128- and 256-output waves, 1, 2 or 4 waves along the outputs of a workgroup and
+  1 or 2 sub-tiles: the same sums in the same order, so the outputs are bit-identical to each other;
 * d_out not a multiple of 8 (the per-element y path), bf16 and fp32 y;
 * a bf16 y that is not 16-byte aligned (the per-element path at d_out = 3072): bit-identical to
   the same call into an aligned y.
@@ -26,7 +26,7 @@ from helpers import random_adapter, rel
 pytestmark = pytest.mark.gpu
 RANK = 16
 REL_BF16 = 2e-3
-MODS = [("down", 12288, 3072), ("odd", 256, 100), ("q", 3072, 3072)]
+MODS = [("down", 12288, 3072), ("odd", 256, 100), ("q", 3072, 3072), ("mid", 512, 640)]
 
 
 @pytest.fixture(scope="module")
@@ -66,23 +66,35 @@ def test_shrink_k_split(bank, monkeypatch, ks):
     assert workspace_errors() == 0
 
 
-@pytest.mark.parametrize("name,d_in,d_out", [("q", 3072, 3072), ("down", 12288, 3072)])
+@pytest.mark.parametrize("name,d_in,d_out", [("q", 3072, 3072), ("down", 12288, 3072), ("mid", 512, 640)])
 def test_expand_tiles_bit_identical(bank, monkeypatch, name, d_in, d_out):
+    """Every expand tile (128 / 256 outputs per wave, 1 / 2 / 4 waves along the outputs, 1 / 2
+    sub-tiles) computes the same sums in the same order: bit-identical outputs, in accumulate and
+    write mode; an empty route writes zeros. d_out = 640 leaves the last workgroup's outer waves
+    past the end of the row."""
     ads, bk, pools = bank
     g = torch.Generator(device="cuda").manual_seed(7)
     x = torch.randn(4, 200, d_in, device="cuda", generator=g).bfloat16()
     y0 = torch.randn(4, 200, d_out, device="cuda", generator=g).bfloat16()
     assign = torch.tensor([1, 3, 0, 1], dtype=torch.int32, device="cuda")
-    outs = []
+    assign_empty = torch.tensor([1, -1, 0, 3], dtype=torch.int32, device="cuda")
+    outs, writes = [], []
     for bo in (128, 256):
-        for subs in (1, 2):
-            monkeypatch.setenv("LITHE_EXPAND_BO", str(bo))
-            monkeypatch.setenv("LITHE_EXPAND_SUBS", str(subs))
-            y = y0.clone()
-            _delta(bk, pools, name, x, assign, 1.0, out=y, accumulate=True)
-            outs.append(y)
+        for wo in (1, 2, 4):
+            for subs in (1, 2):
+                monkeypatch.setenv("LITHE_EXPAND_BO", str(bo))
+                monkeypatch.setenv("LITHE_EXPAND_WO", str(wo))
+                monkeypatch.setenv("LITHE_EXPAND_SUBS", str(subs))
+                y = y0.clone()
+                _delta(bk, pools, name, x, assign, 1.0, out=y, accumulate=True)
+                outs.append(y)
+                writes.append(_delta(bk, pools, name, x, assign_empty, 1.0))
     for y in outs[1:]:
         assert torch.equal(y, outs[0])
+    for w in writes[1:]:
+        assert torch.equal(w, writes[0])
+    assert not writes[0][1].any()
+    assert workspace_errors() == 0
     want = odelta.index_linear(y0.float().cpu().numpy(), _oracle(ads, name, x, assign, d_out, 1.0), "bf16")
     assert rel(outs[0].float().cpu().numpy() - y0.float().cpu().numpy(), want - y0.float().cpu().numpy()) < 1e-2
 
