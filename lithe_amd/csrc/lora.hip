@@ -26,10 +26,9 @@ int env_int(const char *name, int dflt) {
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
 // Launch context of a grouped call: the plan rules that depend on the grid's size (the shrink's K
-// split, the expand's tile width and sub-tiles) see the whole grid of the launch, not one job.
+// split, the expand's sub-tiles) see the whole grid of the launch, not one job.
 struct PlanCtx {
     int64_t groups;     // 16-token groups of every shrink job of the launch
-    int64_t wgs256;     // expand workgroups of every job at 256-output tiles
 };
 
 Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int rank, int n_route, int xbytes,
@@ -88,21 +87,11 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.stage_off = p.red_off + (ks > 1 ? kWaves * p.GMs * 64 * 16 : 0);
     p.lds_s = p.stage_off + (size_t)kWaves * std::min(kStageLoads, kShrinkU) * 1024;
 
-    // expand: BO outputs x 64*subs tokens per workgroup.
+    // expand: a wave computes BO outputs x 16 tokens per sub-tile (the workgroup's layout below).
     int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
     bo_max = std::max(32, bo_max);
-    bool narrow = false;    // 128-output bf16 tiles of the rule below: one sub-tile
-    if (xbytes == 2 && p.GM == 1 && !dense) {
-        // 128-output tiles (76 VGPRs: 6 waves per SIMD with accumulate, against 4) with one
-        // sub-tile where 256-output tiles give fewer than 14,336 workgroups. Measured over the
-        // FLUX shapes: grids of 1,344 to 13,824 workgroups 1-5 % faster, 16,128 and 43,008
-        // slower; dense factors slower (twice the workgroups re-read each B tile)
-        const int64_t wgs256 = ctx ? ctx->wgs256 : n_batch * ((seq + 63) / 64) * ((d_out + 255) / 256);
-        int bo = wgs256 < 14336 ? 128 : 256;
-        if (getenv("LITHE_EXPAND_BO")) bo = env_int("LITHE_EXPAND_BO", bo) == 128 ? 128 : 256;
-        bo_max = bo;
-        narrow = bo == 128;
-    }
+    if (getenv("LITHE_EXPAND_BO") && xbytes == 2 && p.GM == 1 && !dense)
+        bo_max = env_int("LITHE_EXPAND_BO", bo_max) == 128 ? 128 : 256;
     p.U = 4;
     p.BOM = bo_max;
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);
@@ -114,9 +103,10 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // the tokens): a workgroup's y tile is 64 / 2^wo_sh token rows x 2^wo_sh * BO outputs. bf16 y
     // takes two: read-modify-write probes (1 GB of 6 KB / 24 KB rows) moved 64-row x 256 B tiles
     // at 5.53 / 5.60 TB/s, 32 x 256 B at 5.79 / 6.07, 64 x 512 B at 5.78 / 5.82, 32 x 1 KB at
-    // 5.95-6.09 / 6.26-6.42, 2 KB-wide tiles at 5.5-5.8. On the grouped FLUX sweep: 57.7 -> 55.4 ms
-    // (128-output waves 4 along the outputs, 16 x 1 KB tiles: 55.9 ms; 128-output waves 1 along the
-    // outputs: 55.6 ms).
+    // 5.95-6.09 / 6.26-6.42, 2 KB-wide tiles at 5.5-5.8. On the FLUX sweeps (one box): grouped
+    // 57.7 -> 54.9 ms, per module 59.7 -> 58.1 ms with 256-output waves two along the outputs
+    // (32 x 1 KB tiles); 128-output waves two along the outputs (the former rule for grids under
+    // 14,336 workgroups) 0.1-0.4 % slower, four along the outputs 1-2 % slower.
     int wo = ybytes == 2 && !dense ? 2 : 1;
     if (getenv("LITHE_EXPAND_WO")) {
         const int v = env_int("LITHE_EXPAND_WO", 1);
@@ -126,7 +116,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     while (wo > 1 && (int64_t)wo * p.BO > ((d_out + 31) / 32) * 32) wo >>= 1;
     p.wo_sh = wo == 4 ? 2 : wo == 2 ? 1 : 0;
     // (with several waves along the outputs one sub-tile measured faster on every FLUX sweep)
-    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !narrow && !ctx && wo == 1) ? 2 : 1;
+    int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !ctx && wo == 1) ? 2 : 1;
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     const int64_t tps = 64 / wo;     // tokens per sub-tile
@@ -557,9 +547,8 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
     group_layout(n_batch, n_act, mods, G, xbytes, L);
     if (workspace_bytes < L.total) return LITHE_ERR_WORKSPACE;
 
-    PlanCtx ctx{0, 0};
+    PlanCtx ctx{0};
     for (int q = 0; q < L.n_sj; ++q) ctx.groups += n_batch * ((mods[L.mods_of_sj[q][0]].seq + 15) / 16);
-    for (int m = 0; m < n_act; ++m) ctx.wgs256 += n_batch * ((mods[m].seq + 63) / 64) * ((mods[m].d_out + 255) / 256);
 
     // common fields; each job's fields are applied over them
     char *ws = static_cast<char *>(workspace);
