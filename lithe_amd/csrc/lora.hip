@@ -97,8 +97,6 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.BO = (int)std::min<int64_t>(bo_max, ((d_out + 31) / 32) * 32);
     const int64_t o_tiles = (d_out + p.BO - 1) / p.BO;
     const int64_t base_wgs = n_batch * ((seq + 63) / 64) * o_tiles;
-    // 2 sub-tiles of 64 tokens per workgroup only for mid-sized grids (the 512-token, 3072-output
-    // FLUX modules); everywhere else one sub-tile (more, shorter workgroups) measured faster.
     // Waves along the outputs of a workgroup (2^wo_sh of them, BO outputs each; the others along
     // the tokens): a workgroup's y tile is 64 / 2^wo_sh token rows x 2^wo_sh * BO outputs. bf16 y
     // takes two: read-modify-write probes (1 GB of 6 KB / 24 KB rows) moved 64-row x 256 B tiles
@@ -107,15 +105,17 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // 57.7 -> 54.9 ms, per module 59.7 -> 58.1 ms with 256-output waves two along the outputs
     // (32 x 1 KB tiles); 128-output waves two along the outputs (the former rule for grids under
     // 14,336 workgroups) 0.1-0.4 % slower, four along the outputs 1-2 % slower.
-    int wo = ybytes == 2 && !dense ? 2 : 1;
+    // Dense factors too (decoded-mode sweep 62.5 -> 60.6 ms; their B tile is 16 KB at rank 16).
+    int wo = ybytes == 2 ? 2 : 1;
     if (getenv("LITHE_EXPAND_WO")) {
         const int v = env_int("LITHE_EXPAND_WO", 1);
         wo = v >= 4 ? 4 : v >= 2 ? 2 : 1;
     }
-    if (dense) wo = 1;
     while (wo > 1 && (int64_t)wo * p.BO > ((d_out + 31) / 32) * 32) wo >>= 1;
     p.wo_sh = wo == 4 ? 2 : wo == 2 ? 1 : 0;
-    // (with several waves along the outputs one sub-tile measured faster on every FLUX sweep)
+    // 2 sub-tiles per workgroup only for mid-sized grids with one wave along the outputs (fp32 y);
+    // everywhere else one sub-tile (more, shorter workgroups) measured faster, and with two waves
+    // along the outputs one sub-tile was faster on every FLUX sweep.
     int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !ctx && wo == 1) ? 2 : 1;
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
@@ -123,7 +123,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.tiles_e = (int)std::max<int64_t>(1, (seq + tps * subs - 1) / (tps * subs));
     // B periods of one workgroup's outputs: the blocks covering [obase, obase + wo * BO) of a route
     p.nblk_max = (int)(((int64_t)wo * p.BO * rank + kBlock - 1) / kBlock + 1);
-    p.lds_e = kHead + (dense ? (size_t)n_route * p.BO * rank * xbytes : (size_t)n_route * p.nblk_max * 16 * xbytes);
+    p.lds_e = kHead + (dense ? (size_t)n_route * wo * p.BO * rank * xbytes : (size_t)n_route * p.nblk_max * 16 * xbytes);
     // whole-line y path (bf16 y, output tiles of whole lines): a 16 x BOM bf16 tile per wave
     p.estage_off = (int)((p.lds_e + 15) & ~size_t(15));
     if (ybytes == 2 && p.BOM % 64 == 0)
