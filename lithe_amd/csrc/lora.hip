@@ -100,8 +100,8 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // Waves along the outputs of a workgroup (2^wo_sh of them, BO outputs each; the others along
     // the tokens): a workgroup's y tile is 64 / 2^wo_sh token rows x 2^wo_sh * BO outputs. bf16 y
     // takes two: read-modify-write probes (1 GB of 6 KB / 24 KB rows) moved 64-row x 256 B tiles
-    // at 5.53 / 5.60 TB/s, 32 x 256 B at 5.79 / 6.07, 64 x 512 B at 5.78 / 5.82, 32 x 1 KB at
-    // 5.95-6.09 / 6.26-6.42, 2 KB-wide tiles at 5.5-5.8. On the FLUX sweeps (one box): grouped
+    // at 5.53 / 5.60 TB/s, 64 x 512 B at 5.78 / 5.82, 32 x 512 B at 5.79-6.05 / 6.07-6.19, 32 x 1 KB
+    // at 5.95-6.09 / 6.26-6.42, 2 KB-wide tiles at 5.5-5.8. On the FLUX sweeps (one box): grouped
     // 57.7 -> 54.9 ms, per module 59.7 -> 58.1 ms with 256-output waves two along the outputs
     // (32 x 1 KB tiles); 128-output waves two along the outputs (the former rule for grids under
     // 14,336 workgroups) 0.1-0.4 % slower, four along the outputs 1-2 % slower.
