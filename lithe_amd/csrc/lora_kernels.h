@@ -187,6 +187,16 @@ __device__ __forceinline__ void stream_store(V *p, const V &v) {
     else *p = v;
 }
 
+// 8 values as one 16-byte bf16 vector.
+template <typename XT>
+__device__ __forceinline__ void store8(XT *dst, const float *v) {
+    static_assert(sizeof(XT) == 2, "bf16 halves");
+    bf16x8 p;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) p[t] = (__bf16)v[t];
+    *reinterpret_cast<bf16x8 *>(dst) = p;
+}
+
 template <typename XT>
 __device__ __forceinline__ void store16(XT *dst, const float v[16]) {
     if constexpr (sizeof(XT) == 2) {
@@ -237,6 +247,13 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     constexpr int SPB = kBlock / KSTEP;      // k-steps per 64-value block
     constexpr int EV = 16 / sizeof(XT);      // elements per 16-byte vector
     typedef typename std::conditional<kBf16, bf16x8, f32x4>::type XV;
+    // Indexed bf16 factors: row r of a piece holds the first halves of its pb periods, then the
+    // second halves (16-byte units), then one unit of padding. An MFMA's A fragment (lane: row r16,
+    // half gq & 1 of one block) then reads without LDS bank conflicts at pieces of 16 or 48 blocks;
+    // periods stored whole (half h at unit 2 c + h) conflicted 2-way on every read (measured:
+    // SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE 0.5 in probes, 0.16 over the grouped FLUX sweep's
+    // shrinks, 0 after; the sweep time did not change).
+    constexpr bool kSplitHalves = kBf16 && SRC != SRC_DENSE;
 
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay uniform (SGPR) branches
@@ -361,7 +378,13 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
                 const float d = decode_value<fixed_levels<SRC>()>(lut, a.a_src.levels, k, sign_mask(t)) * w;
                 v[t] = live ? d : 0.0f;
             }
-            store16<XT>(reg + gr * a.arow + c * 16, v);
+            if constexpr (kSplitHalves) {
+                // bf16: the two 8-value halves of a period sit pb units apart in the row
+                store8<XT>(reg + gr * a.arow + c * 8, v);
+                store8<XT>(reg + gr * a.arow + (pb + c) * 8, v + 8);
+            } else {
+                store16<XT>(reg + gr * a.arow + c * 16, v);
+            }
             __builtin_amdgcn_sched_barrier(0);    // one item's values live at a time
         }
     };
@@ -490,7 +513,8 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
                 const int u = m * SL + v;
                 const XT *ap;
                 if constexpr (SRC != SRC_DENSE)
-                    ap = reg + g * 16 * a.arow + (kBf16 ? ((sp + u) >> 1) * 16 + 8 * (gq & 1) : ((sp + u) >> 2) * 16 + 4 * gq);
+                    ap = reg + g * 16 * a.arow + (kSplitHalves ? (((sp + u) >> 1) + (gq & 1) * pb) * 8
+                                                  : kBf16 ? ((sp + u) >> 1) * 16 + 8 * (gq & 1) : ((sp + u) >> 2) * 16 + 4 * gq);
                 else
                     ap = reg + g * 16 * a.arow + (sp + u) * KSTEP + (kBf16 ? 8 : 4) * gq;
                 if (u < d.n) av[v][g] = *reinterpret_cast<const XV *>(ap);
