@@ -11,6 +11,8 @@ one expand launch, modules given the same x sharing its shrink.
   grouped launch bit for bit.
 * Modules without tokens are skipped; a group at the real FLUX shapes (B = 14, 4,096 image and
   512 text tokens) equals the per-module calls bit for bit.
+* Rank 32 and 64 (2 and 4 rank groups), a three-entry mixture (three groups), the largest call
+  (8 modules) and fp32 activations (no grouped kernel: job by job) equal the per-module calls.
 """
 import numpy as np
 import pytest
@@ -185,3 +187,107 @@ def test_grouped_flux_double_block_projections_full_size(monkeypatch):
     for n, o, w in zip(names, got, want):
         assert torch.equal(o, w), n
     assert workspace_errors() == 0
+
+
+def _per_module_routes(bk, pools, spec, xs, ys, slots, weights, rank, scale=0.75):
+    """Per-module lithe_lora_delta calls with a mixture route (the grouped call's reference)."""
+    lut_a = _hip.lut_from_pools(pools[0], xs[0].dtype)
+    lut_b = _hip.lut_from_pools(pools[1], xs[0].dtype)
+    for (name, _, _), x, y in zip(spec, xs, ys):
+        _, _, _, a_off, b_off = bk.layout.module(name)
+        f = _delta.indexed_factors(_delta.packed_source(bk.words, 3, a_off), _delta.packed_source(bk.words, 3, b_off),
+                                   lut_a, lut_b)
+        _delta.lora_delta(x, y, rank=rank, factors=f, route=_delta.routes(slots, weights), accumulate=True,
+                          out_scale=scale)
+    torch.cuda.synchronize()
+    return ys
+
+
+@pytest.mark.parametrize("rank", [32, 64])
+def test_grouped_higher_ranks(monkeypatch, rank):
+    """Rank 32 and 64 (2 and 4 rank groups per module: the shrink and expand compiled for 2 and 4
+    groups) in one grouped call: bit-identical to the per-module calls with the same K split."""
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    mods = [("q", 256, 256), ("k", 256, 256), ("aq", 256, 256), ("up", 256, 1024), ("down", 1024, 256)]
+    ads = [random_adapter(mods, rank=rank, seed=900 + s) for s in range(3)]
+    bk, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bk.add(w)
+    pools = (bk.pool_a.bfloat16(), bk.pool_b.bfloat16())
+    g = torch.Generator(device="cuda").manual_seed(rank)
+    spec = [("q", "img", 96), ("k", "img", 96), ("aq", "txt", 40), ("up", "u", 70), ("down", "d", 33)]
+    shape = {n: (di, do) for n, di, do in mods}
+    xs_by_key, xs, ys = {}, [], []
+    for name, key, seq in spec:
+        di, do = shape[name]
+        if key not in xs_by_key:
+            xs_by_key[key] = torch.randn(3, seq, di, device="cuda", generator=g).bfloat16()
+        xs.append(xs_by_key[key])
+        ys.append(torch.randn(3, seq, do, device="cuda", generator=g).bfloat16())
+    slots = torch.tensor([2, 0, 1], dtype=torch.int32, device="cuda")
+    offs = [bk.layout.module(n)[3:5] for n, _, _ in spec]
+    got = [y.clone() for y in ys]
+    prepare_packed_group(xs, got, bk.words, offs, 3, pools, slots, rank, 0.75, shared_workspace("cuda", 64 << 20))()
+    want = [y.clone() for y in ys]
+    for (name, _, _), x, y in zip(spec, xs, want):
+        _, _, sb, a_off, b_off = bk.layout.module(name)
+        packed_lora_delta(x, bk.words, a_off, b_off, 3, pools, slots, rank, sb[0], 0.75, out=y, accumulate=True)
+    torch.cuda.synchronize()
+    for (name, _, _), o, w in zip(spec, got, want):
+        assert torch.equal(o, w), name
+    assert workspace_errors() == 0
+
+
+def test_grouped_three_entry_mixture(bank, monkeypatch):
+    """Three route entries at rank 16: three rank groups (the shrink compiled for exactly three,
+    the expand for four), one with an empty entry; bit-identical to the per-module calls."""
+    _, bk, pools = bank
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    g = torch.Generator(device="cuda").manual_seed(13)
+    spec = [("q", "img", 120), ("k", "img", 120), ("aq", "txt", 50), ("down", "d", 64)]
+    xs, ys = _inputs(spec, g)
+    slots = torch.tensor([[0, 3, 4], [2, -1, 1], [4, 1, 0]], dtype=torch.int32, device="cuda")
+    w = torch.tensor([[0.5, 0.3, 0.2], [0.6, 0.0, 0.4], [0.2, 0.2, 0.6]], device="cuda").sqrt().contiguous()
+    got = _grouped(bk, pools, spec, xs, [y.clone() for y in ys], slots, weights=w)
+    want = _per_module_routes(bk, pools, spec, xs, [y.clone() for y in ys], slots, w, RANK)
+    for (name, _, _), o, r in zip(spec, got, want):
+        assert torch.equal(o, r), name
+    assert workspace_errors() == 0
+
+
+def test_grouped_eight_modules(bank, monkeypatch):
+    """The largest grouped call (8 modules, 8 distinct inputs of different lengths and widths)."""
+    _, bk, pools = bank
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    g = torch.Generator(device="cuda").manual_seed(17)
+    spec = [(n, n, seq) for n, seq in zip(["q", "k", "v", "aq", "ak", "av", "up", "down"],
+                                          [17, 64, 129, 8, 200, 1, 77, 45])]
+    xs, ys = _inputs(spec, g)
+    slots = torch.tensor([4, 1, 2], dtype=torch.int32, device="cuda")
+    got = _grouped(bk, pools, spec, xs, [y.clone() for y in ys], slots)
+    want = _separate(bk, pools, spec, xs, [y.clone() for y in ys], slots)
+    for (name, _, _), o, r in zip(spec, got, want):
+        assert torch.equal(o, r), name
+
+
+def test_grouped_fp32_activations(bank, monkeypatch):
+    """fp32 activations (no grouped kernel: the call runs its jobs one launch at a time through the
+    per-call kernels): bit-identical to the per-module calls."""
+    _, bk, _ = bank
+    pools = (bk.pool_a.float(), bk.pool_b.float())
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    g = torch.Generator(device="cuda").manual_seed(19)
+    spec = [("q", "img", 50), ("k", "img", 50), ("up", "u", 30)]
+    shape = {n: (di, do) for n, di, do in MODS}
+    xs_by_key, xs, ys = {}, [], []
+    for name, key, seq in spec:
+        di, do = shape[name]
+        if key not in xs_by_key:
+            xs_by_key[key] = torch.randn(3, seq, di, device="cuda", generator=g)
+        xs.append(xs_by_key[key])
+        ys.append(torch.randn(3, seq, do, device="cuda", generator=g))
+    slots = torch.tensor([1, 3, 0], dtype=torch.int32, device="cuda")
+    got = _grouped(bk, pools, spec, xs, [y.clone() for y in ys], slots)
+    want = _separate(bk, pools, spec, xs, [y.clone() for y in ys], slots)
+    for (name, _, _), o, r in zip(spec, got, want):
+        assert torch.equal(o, r), name
