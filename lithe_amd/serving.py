@@ -7,7 +7,10 @@
   from one ``PackedBank`` (no per-layer copies; a cold swap into the bank is visible to
   every layer at once). With ``fuse_shared_inputs`` the projections that read one input
   (``to_q`` / ``to_k`` / ``to_v``, ``add_q_proj`` / ``add_k_proj`` / ``add_v_proj``) share
-  one shrink over x (``lithe_lora_delta_shared_x``).
+  one shrink over x in one grouped call (``lithe_lora_delta_grouped``).
+* ``wrap_bank(group_attention=True)`` puts the six q / k / v projections of each FLUX
+  double-block attention into one grouped call made when the attention module is entered
+  (``AttentionGroup``: a forward pre-hook reads ``hidden_states`` and ``encoder_hidden_states``).
 * ``stage_groups`` collects the independent linears of each FLUX block stage (image and text
   projections, the two attention outputs, the two up and the two down projections) into
   ``StageGroup`` objects that add all of a stage's deltas in one grouped call
@@ -20,7 +23,6 @@ Model loading and rendering (diffusers pipelines) are not part of this package.
 """
 from __future__ import annotations
 
-import ctypes
 import weakref
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -28,10 +30,9 @@ import numpy as np
 import torch
 from torch import nn
 
-from .kernels import _delta, _hip
+from .kernels import _hip
 from .kernels.bank import PackedBank
 from .kernels.layers import IndexLoRALinear, PerSampleLoRALinear, replace_module, wrap_linears
-from .kernels.prepared import shared_x_workspace_bytes
 from .module import FLUX_TARGET_MODULES
 from . import codebook as cb
 
@@ -76,7 +77,8 @@ class SharedInputGroup:
     """Bank-backed layers whose linears read the same input (the q / k / v projections).
 
     The first member called with an input computes every member's base output, adds all
-    their deltas with one shrink over x (``lithe_lora_delta_shared_x``), returns its own and
+    their deltas in one grouped call whose members share one shrink over x
+    (``lithe_lora_delta_grouped``: one shrink and one expand launch), returns its own and
     keeps the others until their members are called with the same input tensor (the same
     object at the same version counter, under the same routing tensor and bank generation).
     Any other call recomputes the group and drops what was pending, so results never depend on
@@ -101,24 +103,14 @@ class SharedInputGroup:
         x3 = (x.unsqueeze(1) if squeeze else x).contiguous()
         o3 = [(o.unsqueeze(1) if squeeze else o) for o in outs]
         o3 = [o if o.is_contiguous() else o.contiguous() for o in o3]
-        bsz = x3.shape[0]
-        slots = (torch.zeros((bsz, 1), dtype=torch.int32, device=x.device) if lead.assign is None
+        slots = (torch.zeros((x3.shape[0], 1), dtype=torch.int32, device=x.device) if lead.assign is None
                  else lead.assign.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous())
-        fs = [l._factors(x.dtype) for l in self.layers]
-        n = len(self.layers)
-        lib = _hip.load()
-        need = shared_x_workspace_bytes(tuple(x3.shape), [o.shape[2] for o in o3], lead.rank, 1, x.dtype)
-        ws = _hip.workspace(x.device, need)
-        fa = (_hip.Factors * n)(*fs)
-        ya = (ctypes.c_void_p * n)(*[o.data_ptr() for o in o3])
-        da = (ctypes.c_int64 * n)(*[o.shape[2] for o in o3])
-        sa = (ctypes.c_float * n)(*[l.scaling for l in self.layers])
-        route = _delta.routes(slots)
-        rc = lib.lithe_lora_delta_shared_x(_hip.ptr(x3), _hip.dtype_code(x.dtype), bsz, x3.shape[1], x3.shape[2], n,
-                                           ya, _hip.dtype_code(o3[0].dtype), da, 1, lead.rank, fa,
-                                           ctypes.byref(route), None, sa, _hip.ptr(ws), ws.numel(),
-                                           _hip.stream_of(x.device))
-        _hip.check(rc, "lithe_lora_delta_shared_x")
+        # one grouped call: the members share one shrink job over x (one launch for the shrink,
+        # one for every member's expand)
+        torch.ops.lithe_amd.bank_lora_delta_grouped_(
+            [x3] * len(self.layers), o3, lead._bank[0].words, [l._bank[1] for l in self.layers],
+            [l._bank[2] for l in self.layers], lead.pool_a, lead.pool_b, slots, lead.rank,
+            [l.scaling for l in self.layers])
         return [o.squeeze(1) if squeeze else o for o in o3]
 
     def _state(self, x: torch.Tensor):
@@ -235,11 +227,103 @@ def stage_groups(wrapped: Dict[str, nn.Module]) -> Dict[Tuple[str, str], StageGr
     return groups
 
 
+class AttentionGroup:
+    """The six projections of a FLUX double-block attention (image ``to_q`` / ``to_k`` / ``to_v``
+    over ``hidden_states``, text ``add_q_proj`` / ``add_k_proj`` / ``add_v_proj`` over
+    ``encoder_hidden_states``) added in one grouped call when the attention module is entered.
+
+    A forward pre-hook on the attention module reads the two inputs it is called with (keyword or
+    positional, as diffusers' ``Attention`` takes them), computes the six base outputs and their
+    deltas with one ``StageGroup`` call (the image and text projections each share a shrink), and
+    keeps each output for its projection. A projection called with the input its output was
+    computed from (same tensor object and version, same routing tensor and version, same bank
+    generation) takes it; any other call runs the projection's own per-module forward, so results
+    never depend on how the attention uses its projections. Eager mode: the pending state lives in
+    Python (``torch.compile`` users keep the per-layer ops).
+    """
+
+    def __init__(self, attn: nn.Module, layers: Sequence[IndexLoRALinear]):
+        if len(layers) != 6:
+            raise ValueError("an attention group holds the six q / k / v projections of both streams")
+        self.stage = StageGroup(layers)
+        self.layers = self.stage.layers
+        self._pending: List[Optional[tuple]] = [None] * 6
+        self.calls = 0      # grouped calls made (one per attention entry with both inputs)
+        self.handle = attn.register_forward_pre_hook(self._enter, with_kwargs=True)
+
+    def _state(self, x: torch.Tensor):
+        a = self.layers[0].assign
+        return (x._version, id(a), getattr(a, "_version", None), self.layers[0]._bank[0].generation)
+
+    def _enter(self, module, args, kwargs):
+        h = kwargs.get("hidden_states", args[0] if len(args) > 0 else None)
+        c = kwargs.get("encoder_hidden_states", args[1] if len(args) > 1 else None)
+        self._pending = [None] * 6
+        if not isinstance(h, torch.Tensor) or not isinstance(c, torch.Tensor) or h.shape[0] != c.shape[0]:
+            return None
+        inputs = [h, h, h, c, c, c]
+        outs = self.stage(inputs)
+        self.calls += 1
+        self._pending = [(weakref.ref(x), self._state(x), o) for x, o in zip(inputs, outs)]
+        return None
+
+    def output(self, i: int, x: torch.Tensor) -> torch.Tensor:
+        p = self._pending[i]
+        if p is not None and p[0]() is x and p[1] == self._state(x):
+            self._pending[i] = None
+            return p[2]
+        return self.layers[i](x)
+
+
+class AttentionMember(nn.Module):
+    """Stands in for one projection of an ``AttentionGroup`` (same ``base``, ``assign`` and slots)."""
+
+    def __init__(self, group: AttentionGroup, index: int):
+        super().__init__()
+        self.layer = group.layers[index]
+        self._group = group
+        self._index = index
+
+    @property
+    def base(self) -> nn.Linear:
+        return self.layer.base
+
+    @property
+    def assign(self):
+        return self.layer.assign
+
+    @assign.setter
+    def assign(self, value):
+        self.layer.assign = value
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._group.output(self._index, x)
+
+
 def wrap_bank(model: nn.Module, bank: PackedBank, module_set: str = "all", dtype: Optional[torch.dtype] = None,
-              fuse_shared_inputs: bool = False) -> Dict[str, nn.Module]:
-    """Bank-backed index-resident wrappers for every linear named in the bank's layout."""
+              fuse_shared_inputs: bool = False, group_attention: bool = False) -> Dict[str, nn.Module]:
+    """Bank-backed index-resident wrappers for every linear named in the bank's layout.
+
+    ``group_attention``: the six projections of every attention module that has both streams
+    wrapped run as one grouped call when the module is entered (``AttentionGroup``).
+    ``fuse_shared_inputs``: the q / k / v of every other shared input (single blocks, or double
+    blocks without ``group_attention``) run as one ``SharedInputGroup``."""
     paths = select_paths(bank.layout.names, module_set)
     wrapped = wrap_linears(model, paths, lambda p, lin: IndexLoRALinear.from_bank(lin, bank, p, dtype))
+    if group_attention:
+        for path in list(wrapped):
+            names = STAGES["proj"]
+            if not path.endswith(names[0]):
+                continue
+            prefix = path[: -len(names[0])]
+            members = [prefix + n for n in names]
+            if not all(m in wrapped and isinstance(wrapped[m], IndexLoRALinear) for m in members):
+                continue
+            attn = model.get_submodule((prefix + names[0]).rsplit(".", 1)[0])
+            group = AttentionGroup(attn, [wrapped[m] for m in members])
+            for i, m in enumerate(members):
+                wrapped[m] = AttentionMember(group, i)
+                replace_module(model, m, wrapped[m])
     if fuse_shared_inputs:
         for path in list(wrapped):
             for names in SHARED_INPUT_GROUPS:

@@ -3,7 +3,7 @@
 * ``wrap_index`` (per-layer int32 index stacks, the reference's serving/_common.py:294-306)
   and ``wrap_bank`` (slots read from the packed bank) give bit-equal outputs (same factors,
   same kernels and plan);
-* the shared-input groups (q / k / v through ``lithe_lora_delta_shared_x``) match the unfused
+* the shared-input groups (q / k / v in one grouped call sharing a shrink) match the unfused
   model at the bf16 delta tolerance (the shrink plans split K differently);
 * decoded mode through ``install_decoded_bank`` matches the index-resident model at that
   tolerance (decoded factors are summed from fp32 pools, the fused path's from bf16 pools);
@@ -158,7 +158,7 @@ def _grouped_forward(model, groups, h, c):
     h = torch.cat([c, h], dim=1)
     for i, b in enumerate(model.single_transformer_blocks):
         q, k, v = groups[(f"single_transformer_blocks.{i}.", "proj")]([h, h, h])
-        h = h + q * torch.sigmoid(k) + v
+        h = h + (q * torch.sigmoid(k) + v)
     return h
 
 
@@ -180,3 +180,29 @@ def test_stage_groups_equal_per_module_layers_and_compile(monkeypatch):
         compiled = torch.compile(_grouped_forward, backend="aot_eager", fullgraph=True)(model, groups, h, c)
     assert explain.graph_break_count == 0
     assert torch.equal(compiled, per_module)
+
+
+def test_attention_groups_equal_per_module_layers(monkeypatch):
+    """wrap_bank(group_attention=True): one grouped call per double-block attention entry, every
+    output bit-identical to the per-module layers with the same K split; a projection called outside
+    its attention (or with another tensor) runs its own forward."""
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    model, ads, bank, h, c = _setup(6)
+    m1, m2 = copy.deepcopy(model), copy.deepcopy(model)
+    w1 = serving.wrap_bank(m1, bank)
+    w2 = serving.wrap_bank(m2, bank, group_attention=True)
+    groups = {id(m._group): m._group for m in w2.values() if isinstance(m, serving.AttentionMember)}
+    assert len(groups) == len(m2.transformer_blocks)
+    assign = torch.tensor([3, 1, 0], dtype=torch.int32, device="cuda")
+    serving.set_assign(w1, assign)
+    serving.set_assign(w2, assign)
+    with torch.no_grad():
+        o1, o2 = m1(h, c), m2(h, c)
+        o3 = m2(h, c)
+    assert torch.equal(o2, o1) and torch.equal(o3, o1)
+    assert all(g.calls == 2 for g in groups.values())
+    assert all(p is None for g in groups.values() for p in g._pending)     # every output was taken
+    with torch.no_grad():
+        k_alone = m2.transformer_blocks[0].attn.add_k_proj(c)
+        k_ref = m1.transformer_blocks[0].attn.add_k_proj(c)
+    assert torch.equal(k_alone, k_ref)

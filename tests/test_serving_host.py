@@ -61,3 +61,27 @@ def test_stage_groups_structure(fuse):
     assert len(groups[("transformer_blocks.0.", "down")].layers) == 2
     with pytest.raises(ValueError):
         serving.StageGroup([])
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_wrap_bank_attention_groups_structure(fuse):
+    """group_attention: each double block's six q / k / v projections become stand-ins of one
+    AttentionGroup hooked on its attention module; single blocks keep their q / k / v as shared-input
+    groups (with fuse_shared_inputs) or plain layers; routing reaches every layer."""
+    model = ToyFlux(n_double=2, n_single=2)
+    wrapped = serving.wrap_bank(model, _bank(model), fuse_shared_inputs=fuse, group_attention=True)
+    att = [p for p, m in wrapped.items() if isinstance(m, serving.AttentionMember)]
+    shared = [p for p, m in wrapped.items() if isinstance(m, serving.SharedInputMember)]
+    assert len(att) == 2 * 6 and all(p.startswith("transformer_blocks.") for p in att)
+    assert len(shared) == (2 * 3 if fuse else 0)
+    groups = {id(wrapped[p]._group) for p in att}
+    assert len(groups) == 2
+    attn = model.transformer_blocks[1].attn
+    assert attn.add_k_proj is wrapped["transformer_blocks.1.attn.add_k_proj"]
+    assert len(attn._forward_pre_hooks) == 1
+    assign = torch.tensor([0, 1], dtype=torch.int32)
+    serving.set_assign(wrapped, assign)
+    assert all(m.assign is assign for m in wrapped.values())
+    assert len(serving.stage_groups(wrapped)) == 2 * 4 + 2
+    with pytest.raises(ValueError):
+        serving.AttentionGroup(attn, [wrapped[att[0]].layer])

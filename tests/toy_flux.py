@@ -12,6 +12,9 @@ class _Proj(nn.Module):
 
 
 class _Attn(nn.Module):
+    """Called like diffusers' FLUX attention: ``attn(hidden_states=..., encoder_hidden_states=...)``,
+    every projection reading the tensors passed in (a toy mixing stands in for attention)."""
+
     def __init__(self, d, context=True):
         super().__init__()
         self.to_q, self.to_k, self.to_v = nn.Linear(d, d), nn.Linear(d, d), nn.Linear(d, d)
@@ -19,6 +22,15 @@ class _Attn(nn.Module):
             self.to_out = nn.ModuleList([nn.Linear(d, d)])
             self.add_q_proj, self.add_k_proj, self.add_v_proj = nn.Linear(d, d), nn.Linear(d, d), nn.Linear(d, d)
             self.to_add_out = nn.Linear(d, d)
+
+    def forward(self, hidden_states, encoder_hidden_states=None):
+        h = hidden_states
+        mixed = self.to_q(h) * torch.sigmoid(self.to_k(h)) + self.to_v(h)
+        if encoder_hidden_states is None:
+            return mixed
+        c = encoder_hidden_states
+        mixed_c = self.add_q_proj(c) * torch.sigmoid(self.add_k_proj(c)) + self.add_v_proj(c)
+        return self.to_out[0](mixed), self.to_add_out(mixed_c)
 
 
 class _FF(nn.Module):
@@ -38,11 +50,8 @@ class DoubleBlock(nn.Module):
         self.ff_context = _FF(d, ff)
 
     def forward(self, h, c):
-        a = self.attn
-        q, k, v = a.to_q(h), a.to_k(h), a.to_v(h)
-        h = h + a.to_out[0](q * torch.sigmoid(k) + v)
-        cq, ck, cv = a.add_q_proj(c), a.add_k_proj(c), a.add_v_proj(c)
-        c = c + a.to_add_out(cq * torch.sigmoid(ck) + cv)
+        dh, dc = self.attn(hidden_states=h, encoder_hidden_states=c)
+        h, c = h + dh, c + dc
         return h + self.ff(h), c + self.ff_context(c)
 
 
@@ -52,8 +61,7 @@ class SingleBlock(nn.Module):
         self.attn = _Attn(d, context=False)
 
     def forward(self, h):
-        a = self.attn
-        return h + a.to_q(h) * torch.sigmoid(a.to_k(h)) + a.to_v(h)
+        return h + self.attn(hidden_states=h)
 
 
 class ToyFlux(nn.Module):
