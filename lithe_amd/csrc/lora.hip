@@ -69,16 +69,17 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
         p.pb = std::max(1, (ks >= 4 ? 12 : 4) / p.GM);
         p.arow = p.pb * kBlock + pad;
     } else {
-        // Few token groups (K split over 4 waves): one long piece (fewer barriers) wins; with
-        // whole-K waves the LDS of a long piece costs a workgroup of occupancy, and 16 wins
-        // (measured over the FLUX shapes).
+        // Pieces as long as one fill batch allows: 16 blocks for one rank group (one item per
+        // thread; its registers matter more than the barriers of shorter pieces), up to 48 with
+        // K split over 4 waves and more groups (fewer barriers), 16 with whole-K waves (the LDS of
+        // a longer piece costs a workgroup of occupancy; measured over the FLUX shapes).
         // Three groups: 8-block pieces keep the ring at 26 KB (4 workgroups per CU).
-        p.pb = std::max(1, std::min(ks >= 4 ? 48 : 16, kFillBatch * kThreads / (p.GMs * 16)));
-        if (p.GMs == 3) p.pb = 8;
+        p.pb = std::max(1, std::min(ks >= 4 ? 48 : 16, fill_batch(p.GMs) * kThreads / (p.GMs * 16)));
+        if (p.GMs == 3) p.pb = std::min(8, fill_batch(3) * kThreads / (3 * 16));
         p.arow = p.pb * 16 + pad;
     }
     if (getenv("LITHE_SHRINK_PB")) {
-        p.pb = std::max(1, std::min(env_int("LITHE_SHRINK_PB", p.pb), kFillBatch * kThreads / (p.GMs * 16)));
+        p.pb = std::max(1, std::min(env_int("LITHE_SHRINK_PB", p.pb), fill_batch(p.GMs) * kThreads / (p.GMs * 16)));
         p.arow = p.pb * (dense ? kBlock : 16) + pad;
     }
     p.region = p.GMs * 16 * p.arow;

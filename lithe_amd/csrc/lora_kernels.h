@@ -55,7 +55,11 @@ constexpr int kMaxGroups = 8;
 constexpr int kLutFloats = kMaxLevels * 10;
 constexpr int kHead = 256;
 static_assert(kLutFloats * 4 <= kHead, "LDS head overflow");
-constexpr int kFillBatch = 3;     // fill items per thread whose loads are issued together
+// Fill items per thread whose index loads are issued together (the plan keeps a piece's items
+// within one batch). One rank group: one item (pieces of at most 16 blocks); the two items more
+// cost 30 VGPRs, 4 waves per SIMD instead of 5 (measured: the FLUX sweeps 0.35-0.45 % slower).
+// More groups: three.
+__host__ __device__ constexpr int fill_batch(int gm) { return gm == 1 ? 1 : 3; }
 #ifndef LITHE_SHRINK_U
 #define LITHE_SHRINK_U 4
 #endif
@@ -254,6 +258,7 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     // SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE 0.5 in probes, 0.16 over the grouped FLUX sweep's
     // shrinks, 0 after; the sweep time did not change).
     constexpr bool kSplitHalves = kBf16 && SRC != SRC_DENSE;
+    constexpr int FB = SRC == SRC_DENSE ? 3 : fill_batch(GM);    // dense rows: 16-byte pieces, three per thread
 
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay uniform (SGPR) branches
@@ -332,7 +337,7 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     auto piece_blocks = [&](int g) __attribute__((always_inline)) { return std::min(pb, nb - g * pb); };
 
     // ---- fills. Indexed: item = the 16-value period of (row gr, block c) of piece g, at
-    // most kFillBatch items per thread (the plan keeps GM * 16 * pb <= kFillBatch * kThreads);
+    // most FB items per thread (the plan keeps GM * 16 * pb <= FB * kThreads);
     // the index loads of a piece are issued one piece ahead of its decode.
     // item it of a piece: row gr = it % (GM*16), block c = it / (GM*16) (block-major: a shift)
     auto idx_item = [&](int g, int it, int &gr, int &c, bool &live) __attribute__((always_inline)) -> int64_t {
@@ -346,22 +351,22 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     auto idx_load = [&](int g, RawIdx *dst) __attribute__((always_inline)) {
         if (g >= npiece) return;
         const int items = GM * 16 * piece_blocks(g);
-        int64_t slot[kFillBatch], blk[kFillBatch];
+        int64_t slot[FB], blk[FB];
 #pragma unroll
-        for (int q = 0; q < kFillBatch; ++q) {
+        for (int q = 0; q < FB; ++q) {
             int gr, c;
             bool live;
             blk[q] = idx_item(g, std::min(q * kThreads + tid, items - 1), gr, c, live);
             slot[q] = live ? group_slot(gr >> 4) : 0;
         }
-        load_raw<kFillBatch, SRC == SRC_PACKED, fixed_levels<SRC>()>(a.a_src, slot, blk, dst);
+        load_raw<FB, SRC == SRC_PACKED, fixed_levels<SRC>()>(a.a_src, slot, blk, dst);
     };
     auto idx_store = [&](int g, const RawIdx *src) __attribute__((always_inline)) {
         if (g >= npiece) return;
         const int items = GM * 16 * piece_blocks(g);
         XT *reg = ring + (g & 1) * a.region;
 #pragma unroll
-        for (int q = 0; q < kFillBatch; ++q) {
+        for (int q = 0; q < FB; ++q) {
             const int it = q * kThreads + tid;
             if (it >= items) break;
             int gr, c;
@@ -394,10 +399,10 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
         const int per_row = piece_blocks(g) * (kBlock / EV);
         const int items = GM * 16 * per_row;
         XT *reg = ring + (g & 1) * a.region;
-        for (int base = 0; base < items; base += kFillBatch * kThreads) {
-            f32x4 v[kFillBatch];
+        for (int base = 0; base < items; base += FB * kThreads) {
+            f32x4 v[FB];
 #pragma unroll
-            for (int q = 0; q < kFillBatch; ++q) {
+            for (int q = 0; q < FB; ++q) {
                 const int it = std::min(base + q * kThreads + tid, items - 1);
                 const int gr = it / per_row, c = it - gr * per_row;
                 const int grp = gr >> 4, rr = (grp % a.n_rg) * 16 + (gr & 15);
@@ -407,7 +412,7 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
                 v[q] = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_a) + off);
             }
 #pragma unroll
-            for (int q = 0; q < kFillBatch; ++q) {
+            for (int q = 0; q < FB; ++q) {
                 const int it = base + q * kThreads + tid;
                 if (it >= items) break;
                 const int gr = it / per_row, c = it - gr * per_row;
@@ -547,9 +552,9 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
 
     // ---- prologue: index loads of pieces 0 and 1, then x of the first two batches; the
     // decode below waits for its own loads only (loads complete in order).
-    RawIdx raw[kFillBatch];
+    RawIdx raw[FB];
     {
-        RawIdx raw1[kFillBatch];
+        RawIdx raw1[FB];
         if constexpr (SRC != SRC_DENSE) {
             idx_load(0, raw);
             idx_load(1, raw1);
@@ -588,7 +593,8 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
                 ++pg;
             }
         };
-        // batch i sits in ba (i even) or bb (i odd); batch i + 1 is in flight in the other
+        // batch i sits in ba (i even) or bb (i odd); batch i + 1 is in flight in the other (a third
+        // batch in flight measured no faster on the FLUX sweeps)
         while (da.n > 0) {
             enter(da.g);
             compute_batch(ba, da);
