@@ -28,7 +28,7 @@ from helpers import random_adapter, rel
 pytestmark = pytest.mark.gpu
 RANK = 16
 MODS = [("q", 256, 256), ("k", 256, 256), ("v", 256, 256), ("aq", 256, 256), ("ak", 256, 256), ("av", 256, 256),
-        ("up", 256, 1024), ("down", 1024, 256)]
+        ("up", 256, 1024), ("down", 1024, 256), ("mid", 512, 640)]
 
 
 @pytest.fixture(scope="module")
@@ -291,3 +291,21 @@ def test_grouped_fp32_activations(bank, monkeypatch):
     want = _separate(bk, pools, spec, xs, [y.clone() for y in ys], slots)
     for (name, _, _), o, r in zip(spec, got, want):
         assert torch.equal(o, r), name
+
+
+def test_grouped_partial_tiles(bank, monkeypatch):
+    """Token counts that fill no tile evenly and d_out = 640 (its second 512-output workgroup has
+    one wave past the end of the row), in write and accumulate mode: bit-identical to the
+    per-module calls."""
+    _, bk, pools = bank
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    g = torch.Generator(device="cuda").manual_seed(23)
+    spec = [("mid", "m", 37), ("q", "q", 45), ("down", "d", 3)]
+    xs, ys = _inputs(spec, g)
+    slots = torch.tensor([3, 2, 0], dtype=torch.int32, device="cuda")
+    for acc in (True, False):
+        got = _grouped(bk, pools, spec, xs, [y.clone() for y in ys], slots, accumulate=acc)
+        want = _separate(bk, pools, spec, xs, [y.clone() for y in ys], slots, accumulate=acc)
+        for (name, _, _), o, r in zip(spec, got, want):
+            assert torch.equal(o, r), (name, acc)
+    assert workspace_errors() == 0
