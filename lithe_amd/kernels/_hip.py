@@ -196,6 +196,12 @@ _CLASSES = _popcount_classes(64, 9)
 _lut_cache: Dict[int, Dict[Tuple, Lut]] = {}
 
 
+def version_of(t: torch.Tensor):
+    """The tensor's version counter, or None for an inference tensor (``torch.inference_mode``
+    tensors keep none; they cannot be written outside inference mode)."""
+    return None if t.is_inference() else t._version
+
+
 def lut_from_pools(pools: torch.Tensor, dtype: Optional[torch.dtype] = None) -> Lut:
     """Value table of a (L, 512, 64) pool stack after casting it to ``dtype``.
 
@@ -209,7 +215,7 @@ def lut_from_pools(pools: torch.Tensor, dtype: Optional[torch.dtype] = None) -> 
     if not 1 <= L <= 4:
         raise ValueError("num_levels must be in [1, 4]")
     dtype = dtype or pools.dtype
-    key = (pools._version, pools.dtype, dtype)
+    key = (version_of(pools), pools.dtype, dtype)
     per = _lut_cache.get(id(pools))
     if per is not None and key in per:
         return per[key]

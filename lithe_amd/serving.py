@@ -80,7 +80,9 @@ class SharedInputGroup:
     their deltas in one grouped call whose members share one shrink over x
     (``lithe_lora_delta_grouped``: one shrink and one expand launch), returns its own and
     keeps the others until their members are called with the same input tensor (the same
-    object at the same version counter, under the same routing tensor and bank generation).
+    object at the same version counter, under the same routing tensor and bank generation; an
+    inference-mode tensor has no version counter, so an in-place write into it between its members'
+    calls is not seen).
     Any other call recomputes the group and drops what was pending, so results never depend on
     the call order.
     """
@@ -118,7 +120,8 @@ class SharedInputGroup:
         version, the routing tensor and its version, and the bank's generation (bumped by every
         write into a slot)."""
         a = self.layers[0].assign
-        return (x._version, id(a), getattr(a, "_version", None), self.layers[0]._bank[0].generation)
+        return (_hip.version_of(x), id(a), _hip.version_of(a) if isinstance(a, torch.Tensor) else None,
+                self.layers[0]._bank[0].generation)
 
     def output(self, i: int, x: torch.Tensor) -> torch.Tensor:
         state = self._state(x)
@@ -253,7 +256,8 @@ class AttentionGroup:
 
     def _state(self, x: torch.Tensor):
         a = self.layers[0].assign
-        return (x._version, id(a), getattr(a, "_version", None), self.layers[0]._bank[0].generation)
+        return (_hip.version_of(x), id(a), _hip.version_of(a) if isinstance(a, torch.Tensor) else None,
+                self.layers[0]._bank[0].generation)
 
     def _enter(self, module, args, kwargs):
         h = kwargs.get("hidden_states", args[0] if len(args) > 0 else None)

@@ -206,3 +206,20 @@ def test_attention_groups_equal_per_module_layers(monkeypatch):
         k_alone = m2.transformer_blocks[0].attn.add_k_proj(c)
         k_ref = m1.transformer_blocks[0].attn.add_k_proj(c)
     assert torch.equal(k_alone, k_ref)
+
+
+def test_grouped_serving_under_inference_mode(monkeypatch):
+    """Shared-input and attention groups under torch.inference_mode (inference tensors keep no
+    version counter): the same outputs as the per-module layers."""
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    model, ads, bank, h, c = _setup(7)
+    m1, m2 = copy.deepcopy(model), copy.deepcopy(model)
+    w1 = serving.wrap_bank(m1, bank)
+    w2 = serving.wrap_bank(m2, bank, fuse_shared_inputs=True, group_attention=True)
+    assign = torch.tensor([0, 2, 3], dtype=torch.int32, device="cuda")
+    serving.set_assign(w1, assign)
+    serving.set_assign(w2, assign)
+    with torch.inference_mode():
+        hi, ci = h.clone(), c.clone()
+        o1, o2 = m1(hi, ci), m2(hi, ci)
+    assert torch.equal(o2, o1)
