@@ -682,8 +682,9 @@ def run_encode(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 20; 200 for --config ffn, "
+                    "whose step is 0.35 ms)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 3; 20 for --config ffn)")
     ap.add_argument("--config", default="grouped",
                     choices=["grouped", "flux342", "fused", "qkv", "decoded", "ffn", "hb", "hb_modules", "decode",
                              "ingest", "encode"])
@@ -692,6 +693,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--slots", type=int, default=None, help="bank size (default: the configuration's)")
     args = ap.parse_args()
+    short = args.config == "ffn"
+    args.steps = args.steps if args.steps is not None else (200 if short else 20)
+    args.warmup = args.warmup if args.warmup is not None else (20 if short else 3)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path needs no "
               "collective: samples shard across GPUs with no exchange).", file=sys.stderr)
