@@ -300,16 +300,20 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     }
     if (tid < GM && tid < a.G) route_slot(a, b, (tid % a.G1) / a.n_rg, true);   // records bad slot ids
     if (!any) return;    // no adapter on this sample: no mid row is read for it
-    auto group_slot = [&](int g) __attribute__((always_inline)) -> int32_t {    // gs[g] for a run-time g < GM
+    // gs[g] / gw[g] for a per-lane g < GM: a select chain over the (uniform) values. Passing them
+    // through readfirstlane keeps the compiler from folding the chain back into an indexed load of
+    // the local array, which would put the array in scratch (28-80 bytes per lane at 3-8 groups).
+    auto group_slot = [&](int g) __attribute__((always_inline)) -> int32_t {
         int32_t r = gs[0];
 #pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? gs[q] : r;
+        for (int q = 1; q < GM; ++q) r = g == q ? __builtin_amdgcn_readfirstlane(gs[q]) : r;
         return r;
     };
     auto group_weight = [&](int g) __attribute__((always_inline)) -> float {
         float r = gw[0];
 #pragma unroll
-        for (int q = 1; q < GM; ++q) r = g == q ? gw[q] : r;
+        for (int q = 1; q < GM; ++q)
+            r = g == q ? __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, gw[q]))) : r;
         return r;
     };
     auto group_rank0 = [&](int g) __attribute__((always_inline)) -> int {   // (g % n_rg) * 16
