@@ -205,7 +205,12 @@ def test_attention_groups_equal_per_module_layers(monkeypatch):
     with torch.no_grad():
         k_alone = m2.transformer_blocks[0].attn.add_k_proj(c)
         k_ref = m1.transformer_blocks[0].attn.add_k_proj(c)
+        g0 = m2.transformer_blocks[0].attn.to_q._group
+        before = g0.calls
+        pos = m2.transformer_blocks[0].attn(h, c)              # positional arguments reach the hook too
+        ref = m1.transformer_blocks[0].attn(h, c)
     assert torch.equal(k_alone, k_ref)
+    assert g0.calls == before + 1 and all(torch.equal(p, r) for p, r in zip(pos, ref))
 
 
 def test_grouped_serving_under_inference_mode(monkeypatch):
