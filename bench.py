@@ -91,7 +91,7 @@ class Workload:
     """Bank, buffers and prepared per-module calls of one configuration."""
 
     def __init__(self, name, mods, batch, n_slots, assign, layout_mods=None, seed=0, decoded=False, qkv=False,
-                 grouped=False):
+                 grouped=False, rank=RANK):
         import numpy as np
         import torch
 
@@ -104,7 +104,7 @@ class Workload:
         dev = torch.device("cuda:0")
         layout_mods = layout_mods or mods
         layout = PackedLayout.from_modules(
-            [{"name": n, "shape_a": [RANK, di], "shape_b": [do, RANK]} for n, di, do, _ in layout_mods],
+            [{"name": n, "shape_a": [rank, di], "shape_b": [do, rank]} for n, di, do, _ in layout_mods],
             num_levels=3, block_size=64, scaling=1.0)
         self.bank = PackedBank(layout, dev, capacity=n_slots)
         self.bank.fill_random(n_slots, generator=torch.Generator(device=dev).manual_seed(seed))
@@ -135,13 +135,13 @@ class Workload:
             pool.append(torch.randn(batch, m, d, device=dev, generator=gen).to(torch.bfloat16))
             return pool[-1]
 
-        need = max(workspace_bytes((batch, m, di), do, RANK, 3 if qkv else 1, torch.bfloat16) for _, di, do, m in mods)
+        need = max(workspace_bytes((batch, m, di), do, rank, 3 if qkv else 1, torch.bfloat16) for _, di, do, m in mods)
         groups = flux_groups(mods) if grouped else []
         for gi in groups:
             keys = [_SHARED_INPUT.get(_split(mods[i][0])[1], str(i)) if qkv else str(i) for i in gi]
             ids = {k: j for j, k in enumerate(dict.fromkeys(keys))}
             need = max(need, group_workspace_bytes([(mods[i][3], mods[i][1], mods[i][2]) for i in gi],
-                                                   [ids[k] for k in keys], batch, RANK, 1, torch.bfloat16))
+                                                   [ids[k] for k in keys], batch, rank, 1, torch.bfloat16))
         self.workspace = shared_workspace(dev, need)
         self.calls = []
         self.call_mods = []
@@ -171,7 +171,7 @@ class Workload:
                 xs.append(shared[key] if key is not None else x)
                 ys.append(buf(do, m, xs + ys))
                 offs.append(layout.module(n)[3:5])
-            self.calls.append(prepare_packed_group(xs, ys, self.bank.words, offs, 3, pools, self.assign, RANK, 1.0,
+            self.calls.append(prepare_packed_group(xs, ys, self.bank.words, offs, 3, pools, self.assign, rank, 1.0,
                                                    self.workspace, accumulate=True))
             self.call_mods.append([mods[i] for i in gi])
         k = len(mods) if grouped else 0
@@ -185,7 +185,7 @@ class Workload:
                 for g in group:
                     ys.append(buf(g[2], g[3], [x] + ys))
                 offs = [layout.module(g[0])[3:5] for g in group]
-                self.calls.append(prepare_packed_shared_x(x, ys, self.bank.words, offs, 3, pools, self.assign, RANK,
+                self.calls.append(prepare_packed_shared_x(x, ys, self.bank.words, offs, 3, pools, self.assign, rank,
                                                           1.0, self.workspace, accumulate=True))
                 self.call_mods.append(group)
                 k += 3
@@ -197,13 +197,13 @@ class Workload:
             y = buf(do, m, [x])
             if decoded:
                 a, b = self.factors[n]
-                self.calls.append(prepare_dense(x, y, a, b, self.sel, RANK, 1.0, self.workspace, accumulate=True))
+                self.calls.append(prepare_dense(x, y, a, b, self.sel, rank, 1.0, self.workspace, accumulate=True))
             else:
-                self.calls.append(prepare_packed(x, y, self.bank.words, a_off, b_off, 3, pools, self.assign, RANK,
+                self.calls.append(prepare_packed(x, y, self.bank.words, a_off, b_off, 3, pools, self.assign, rank,
                                                  1.0, self.workspace, accumulate=True))
         self.tokens = batch * max(m for _, _, _, m in mods) if name != "ffn" else batch * mods[0][3]
         if decoded:   # dense factors of the routed adapters instead of their packed words
-            self.index_bytes = len(uniq) * sum(2 * RANK * (di + do) for _, di, do, _ in mods)
+            self.index_bytes = len(uniq) * sum(2 * rank * (di + do) for _, di, do, _ in mods)
         else:
             self.index_bytes = len(uniq) * layout.num_words * 8
         self.alg_bytes = sum(c.algorithmic_bytes() for c in self.calls) + self.index_bytes
@@ -325,7 +325,7 @@ def environment() -> dict:
             "host_threads": host_threads()}
 
 
-def cpu_baseline(mods, batch, n_slots, budget_s=20.0):
+def cpu_baseline(mods, batch, n_slots, budget_s=20.0, rank=RANK):
     """The reference's serving forward restated in torch CPU ops (oracle.torch_cpu: fp32
     gather-sum decode of the routed adapters every forward, alpha / r folded into B, two bf16
     torch.bmm, the add into the base output) on the host cores.
@@ -351,7 +351,7 @@ def cpu_baseline(mods, batch, n_slots, budget_s=20.0):
     passes = 0
     while True:
         for (di, do, m) in sorted(classes):
-            nba, nbb = RANK * di // 64, do * RANK // 64
+            nba, nbb = rank * di // 64, do * rank // 64
             ia = [torch.randint(0, 512, (3, nba), generator=g, dtype=torch.int16) for _ in range(batch)]
             ib = [torch.randint(0, 512, (3, nbb), generator=g, dtype=torch.int16) for _ in range(batch)]
             x = torch.randn(batch, m, di, generator=g).bfloat16()
@@ -360,7 +360,7 @@ def cpu_baseline(mods, batch, n_slots, budget_s=20.0):
             w = torch.ones(batch, 1)
             scales = torch.ones(batch)
             t = time.perf_counter()
-            torch_cpu.routed_add(x, y, ids, w, ia, ib, scales, pa, pb, RANK)
+            torch_cpu.routed_add(x, y, ids, w, ia, ib, scales, pa, pb, rank)
             dt = time.perf_counter() - t
             per_class[(di, do, m)] = min(per_class.get((di, do, m), dt), dt)
             del x, y
@@ -688,7 +688,8 @@ def main():
     ap.add_argument("--config", default="grouped",
                     choices=["grouped", "flux342", "fused", "qkv", "decoded", "ffn", "hb", "hb_modules", "decode",
                              "ingest", "encode"])
-    ap.add_argument("--rank", type=int, default=RANK, help="rank of the decode configuration (16 or 64)")
+    ap.add_argument("--rank", type=int, default=RANK, help="adapter rank (a multiple of 16; the headline and the "
+                    "decode's first line are rank 16, its second rank 64)")
     ap.add_argument("--no-graph", action="store_true", help="launch every call from Python instead of a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--slots", type=int, default=None, help="bank size (default: the configuration's)")
@@ -723,7 +724,8 @@ def main():
         mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
         assign = rng.choice(n_slots, batch, replace=False)
         wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config == "decoded",
-                      qkv=args.config in ("qkv", "fused"), grouped=args.config in ("grouped", "fused"))
+                      qkv=args.config in ("qkv", "fused"), grouped=args.config in ("grouped", "fused"),
+                      rank=args.rank)
         workload = "FLUX.1-dev 342 linears, 1024^2: B=14 x 4608 tokens (4096 img + 512 txt), 10k-adapter packed bank"
         if args.config == "decoded":
             workload += (", decoded mode: the 14 routed adapters decoded once to stacked bf16 factors "
@@ -742,7 +744,7 @@ def main():
         p /= p.sum()
         perm = rng.permutation(n_slots)
         assign = perm[rng.choice(n_slots, batch, p=p)]
-        wl = Workload("hb", mods, batch, n_slots, assign, grouped=args.config == "hb")
+        wl = Workload("hb", mods, batch, n_slots, assign, grouped=args.config == "hb", rank=args.rank)
         workload = "FLUX.1-dev 342 linears, 256^2: B=96 x 768 tokens (256 img + 512 txt), Zipf(1.1) over 10k bank"
         workload += (", grouped: one shrink + one expand launch per block stage" if args.config == "hb"
                      else ", one call per module") + f" ({len(wl.calls)} calls per sweep)"
@@ -752,9 +754,11 @@ def main():
                 ("transformer_blocks.0.ff.net.2", 12288, 3072, 1536)]
         batch, n_slots = 14, args.slots or 1_000
         assign = rng.choice(n_slots, batch, replace=False)
-        wl = Workload("ffn", mods, batch, n_slots, assign, layout_mods=full)
+        wl = Workload("ffn", mods, batch, n_slots, assign, layout_mods=full, rank=args.rank)
         workload = "FLUX FFN pair 3072->12288->3072 at 512^2: B=14 x 1536 tokens, 1k-adapter packed bank"
 
+    if args.rank != RANK:
+        workload += f", rank {args.rank}"
     ms, graphed = time_sweeps(wl, args.steps, args.warmup, not args.no_graph)
     # the kernels record bad slot ids and out-of-range indices in the workspace's error word
     import ctypes
@@ -788,11 +792,11 @@ def main():
         del e["bytes"]
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and args.rank == RANK:     # the committed counter runs are rank 16
         with open(tpath) as fh:
             traffic = json.load(fh).get("hbm_bytes_per_launch")
     copy_gbps = copy_bandwidth_gbps()
-    cpu = None if args.no_cpu else cpu_baseline(wl.mods, batch, n_slots)
+    cpu = None if args.no_cpu else cpu_baseline(wl.mods, batch, n_slots, rank=args.rank)
     line = {
         "metric": "adapter-delta tokens/s + achieved HBM GB/s (% peak), FLUX linears, B=14 mixed",
         "value": round(value, 1),
@@ -807,7 +811,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": workload, "modules": len(wl.mods), "global_batch": batch,
-                   "tokens_per_step": tokens, "rank": RANK, "bank_slots": n_slots,
+                   "tokens_per_step": tokens, "rank": args.rank, "bank_slots": n_slots,
                    "bank_GB": round(wl.bank.words.numel() * 8 / 1e9, 2), "hip_graph": graphed,
                    "calls_per_step": len(wl.calls)},
         "achieved_GBps": round(wl.alg_bytes / (ms * 1e-3) / 1e9, 1),
