@@ -88,10 +88,20 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.stage_off = p.red_off + (ks > 1 ? kWaves * p.GMs * 64 * 16 : 0);
     p.lds_s = p.stage_off + (size_t)kWaves * std::min(kStageLoads, kShrinkU) * 1024;
 
+    // expand rank collapse (bf16 activations, packed or indexed factors): the NS rank groups of an
+    // output that share one 64-value factor block are summed before the MFMA (expand_body);
+    // rank 64 / 128: sets of 4, rank 32 / 96: pairs. LITHE_EXPAND_NS=1 turns it off.
+    p.NS = 1;
+    if (xbytes == 2 && !dense && rank % 32 == 0) p.NS = rank % 64 == 0 ? 4 : 2;
+    if (const char *v = getenv("LITHE_EXPAND_NS"))
+        if (atoi(v) == 1) p.NS = 1;
+    const int ge = p.G / p.NS;
+    p.GE = ge <= 1 ? 1 : ge <= 2 ? 2 : ge <= 4 ? 4 : 8;
+
     // expand: a wave computes BO outputs x 16 tokens per sub-tile (the workgroup's layout below).
-    int bo_max = xbytes == 2 ? std::min(256, 512 / p.GM) : std::min(128, 256 / p.GM);
+    int bo_max = xbytes == 2 ? std::min(256, 512 / p.GE) : std::min(128, 256 / p.GE);
     bo_max = std::max(32, bo_max);
-    if (getenv("LITHE_EXPAND_BO") && xbytes == 2 && p.GM == 1 && !dense)
+    if (getenv("LITHE_EXPAND_BO") && xbytes == 2 && p.GE == 1 && p.NS == 1 && !dense)
         bo_max = env_int("LITHE_EXPAND_BO", bo_max) == 128 ? 128 : 256;
     p.U = 4;
     p.BOM = bo_max;
@@ -114,10 +124,20 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     }
     while (wo > 1 && (int64_t)wo * p.BO > ((d_out + 31) / 32) * 32) wo >>= 1;
     p.wo_sh = wo == 4 ? 2 : wo == 2 ? 1 : 0;
-    // 2 sub-tiles per workgroup only for mid-sized grids with one wave along the outputs (fp32 y);
-    // everywhere else one sub-tile (more, shorter workgroups) measured faster, and with two waves
-    // along the outputs one sub-tile was faster on every FLUX sweep.
+    // One rank group: 2 sub-tiles per workgroup only for mid-sized grids with one wave along the
+    // outputs (fp32 y); everywhere else one sub-tile (more, shorter workgroups) measured faster,
+    // and with two waves along the outputs one sub-tile was faster on every FLUX sweep.
     int subs = (base_wgs >= 4 * 256 && base_wgs < 16 * 256 && !ctx && wo == 1) ? 2 : 1;
+    // Several rank groups: the B tile a workgroup builds (n_route * rank / 2 bytes of periods per
+    // output) grows with the groups, its y tile (64 bytes per output and sub-tile) does not, so
+    // more tokens per workgroup amortize it: the tile ratio is G / 8. Grouped FLUX sweeps (bf16,
+    // packed, rank collapse): rank 32 63.3 -> 60.6 ms and rank 64 83.0 -> 73.9 ms with 2 sub-tiles
+    // (4: slower), rank 128 142.1 -> 127.5 ms with 4. Without the collapse (one MFMA per rank
+    // group) rank 32 was best at 2 (72.2 -> 60.8 ms), rank 64 at 4 to 8 (130.6 -> 83.3 / 80.7 ms).
+    if (p.G >= 2) {
+        const int sg = (p.G >= 8 || (p.G >= 4 && p.NS == 1)) ? 4 : 2;
+        if (base_wgs >= (int64_t)sg * 1024) subs = std::max(subs, sg);
+    }
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;
     const int64_t tps = 64 / wo;     // tokens per sub-tile
@@ -665,7 +685,7 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
     const bool grouped = getenv("LITHE_GROUPED_SERIAL") == nullptr;
     if (grouped && launch_shrink_group_bf16_ok(x_dtype, y_dtype, src)) {
         launch_shrink_group_bf16(ps[0].GMs, gs, (unsigned)grid_s, lds_s, src, st);
-        launch_expand_group_bf16_bf16(pe[0].GM, pe[0].BOM, ge, (unsigned)grid_e, lds_e, src, st);
+        launch_expand_group_bf16_bf16(pe[0].GE, pe[0].BOM, pe[0].NS, ge, (unsigned)grid_e, lds_e, src, st);
     } else {
         // job by job through the per-call kernels (other dtypes and factor kinds)
         for (int k = 0; k < gs.n_jobs; ++k) {

@@ -10,10 +10,10 @@ void launch_expand_bf16_bf16(const Plan &p, const LoraArgs &a, int src, hipStrea
     else dispatch_expand<__bf16, __bf16, SRC_INDEXED>(p, a, st);
 }
 
-bool launch_expand_group_bf16_bf16(int GM, int BOM, const GroupArgs &g, unsigned grid, size_t lds, int src,
+bool launch_expand_group_bf16_bf16(int GM, int BOM, int NS, const GroupArgs &g, unsigned grid, size_t lds, int src,
                                    hipStream_t st) {
     if (src != SRC_PACKED) return false;
-    dispatch_expand_group<__bf16, __bf16, SRC_PACKED>(GM, BOM, g, grid, lds, st);
+    dispatch_expand_group<__bf16, __bf16, SRC_PACKED>(GM, BOM, NS, g, grid, lds, st);
     return true;
 }
 

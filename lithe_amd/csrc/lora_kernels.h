@@ -126,6 +126,7 @@ struct Plan {
     int tiles_s, ks, pb, arow, region, red_off, stage_off;
     size_t lds_s, lds_e;
     int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off, wo_sh;
+    int NS, GE;    // expand: rank groups summed per effective group (rank collapse), effective groups (power of two)
     int64_t off_mid, total;
 };
 
@@ -687,12 +688,22 @@ template <> struct Y8<float> {
     }
 };
 
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+// Rank collapse (NS > 1, bf16 activations, packed or indexed factors). Every decoded 64-value
+// block is four copies of one 16-value period: value p of a codebook entry is a sum over the
+// generator columns q = 0..8 of H64[p][q] = (-1)^popcount(p & q), which depends on p only
+// through p & 15. B row o holds ranks o * rank + r of the flat factor, so when rank is a multiple
+// of 16 NS, the NS rank groups 16 (NS e) .. 16 (NS e + NS) - 1 of output o lie in one block and
+// have equal B fragments: sum_g mid[g] . P = (sum_g mid[g]) . P. The expand then sums the NS mid
+// fragments of each such set in fp32, splits the sum s into bf16 hi = bf16(s) and lo = bf16(s - hi)
+// (|s - hi - lo| <= 2^-17 |s|) and runs one 16x16x32 MFMA on K = (hi, lo) against (P, P): GM
+// counts these sets ("effective groups", each NS groups of one route), not the rank groups.
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS = 1>
 __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
+    static_assert(NS == 1 || (sizeof(XT) == 2 && SRC != SRC_DENSE && QUAD), "rank collapse: bf16, indexed factors");
     // bf16 y with output tiles of whole lines: the whole-line y path (line_subtile below)
     constexpr bool LINE = sizeof(YT) == 2 && BOM % 64 == 0;
-    typedef typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type Frag;
+    typedef typename std::conditional<NS != 1, bf16x8, typename std::conditional<sizeof(XT) == 2, i16x4, f32x4>::type>::type Frag;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, r16 = lane & 15, gq = lane >> 4;
@@ -714,7 +725,7 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     bool any = false;
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-        gslot[g] = g < a.G ? route_slot(a, b, g / a.n_rg, false) : -1;
+        gslot[g] = g * NS < a.G ? route_slot(a, b, g * NS / a.n_rg, false) : -1;
         any = any || gslot[g] >= 0;
     }
     auto sub_row = [&](int sub, bool &valid) __attribute__((always_inline)) -> int64_t {
@@ -777,11 +788,11 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     for (int g = 0; g < GM; ++g) gsrc[g] = gslot[g] >= 0 ? g : 0;
 
     // Per-route B multipliers (scalar loads: b and the route are uniform). Route j's first
-    // rank group is g = j * n_rg.
+    // rank group is j * n_rg (effective group j * n_rg / NS).
     float gw[GM], gsc[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-        const int j = (g < a.G ? g : 0) / a.n_rg;
+        const int j = (g * NS < a.G ? g * NS : 0) / a.n_rg;
         gw[g] = a.r_w ? a.r_w[b * a.n_route + j] : 1.0f;
         gsc[g] = (gslot[g] >= 0 && a.s_scale) ? a.s_scale[gslot[g]] : 1.0f;
     }
@@ -792,9 +803,9 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
         sc = gsc[0];
 #pragma unroll
         for (int q = 1; q < GM; ++q) {
-            slot = g0 == q ? gslot[q] : slot;
-            w = g0 == q ? gw[q] : w;
-            sc = g0 == q ? gsc[q] : sc;
+            slot = g0 == q * NS ? gslot[q] : slot;
+            w = g0 == q * NS ? gw[q] : w;
+            sc = g0 == q * NS ? gsc[q] : sc;
         }
     };
 
@@ -901,6 +912,14 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     };
     auto bfrag = [&](int p, int h, int g) __attribute__((always_inline)) -> Frag {
         const int64_t o = obase + 32 * p + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+        if constexpr (NS != 1) {
+            // half gq & 1 of the period of output o and effective group g (K = (P, P))
+            const int gg = g * NS < a.G ? g * NS : 0;
+            const bool live = p < np && gslot[g] >= 0 && o < o_end;
+            const i16x8 fr = *reinterpret_cast<const i16x8 *>(
+                bp + b_index(gg / a.n_rg, live ? o : obase, (gg % a.n_rg) * 16) + 8 * (gq & 1));
+            return __builtin_bit_cast(Frag, live ? fr : i16x8{});
+        }
         const int gg = g < a.G ? g : 0;
         const int j = gg / a.n_rg;
         const int rr = (gg % a.n_rg) * 16 + 4 * gq;
@@ -933,11 +952,16 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
 #pragma unroll
             for (int g = 0; g < GM; ++g) {
                 // a group without an adapter contributes exact zeros (its mid slot is not written)
-                const Frag m = gslot[g] >= 0 ? mf[g] : Frag{};
                 const Frag bf = bfrag(p, h, g);
-                if constexpr (sizeof(XT) == 2) {
+                if constexpr (NS != 1) {
+                    const Frag m = __builtin_bit_cast(
+                        Frag, gslot[g] >= 0 ? __builtin_bit_cast(i16x8, mf[g]) : i16x8{});
+                    acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, m, acc[h], 0, 0, 0);
+                } else if constexpr (sizeof(XT) == 2) {
+                    const Frag m = gslot[g] >= 0 ? mf[g] : Frag{};
                     acc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bf, m, acc[h], 0, 0, 0);
                 } else {
+                    const Frag m = gslot[g] >= 0 ? mf[g] : Frag{};
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         acc[h] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[e], m[e], acc[h], 0, 0, 0);
@@ -1016,9 +1040,29 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
         Frag mf[GM];
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
-            const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + (a.mid_goff + gsrc[g]) * 16 + 4 * gq;
-            if constexpr (sizeof(XT) == 2) mf[g] = *reinterpret_cast<const i16x4 *>(src);
-            else mf[g] = *reinterpret_cast<const f32x4 *>(src);
+            if constexpr (NS != 1) {
+                // lane (token r16, gq): values 8 (gq & 1) .. + 7 of the sum of the NS groups' mid
+                // fragments, its bf16 hi part (gq < 2) or lo part (gq >= 2)
+                const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + (a.mid_goff + gsrc[g] * NS) * 16 + 8 * (gq & 1);
+                float s[8];
+#pragma unroll
+                for (int q = 0; q < NS; ++q) {
+                    const bf16x8 v = *reinterpret_cast<const bf16x8 *>(src + q * 16);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) s[e] = q == 0 ? (float)v[e] : s[e] + (float)v[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const __bf16 hi = (__bf16)s[e];
+                    mf[g][e] = gq < 2 ? hi : (__bf16)(s[e] - (float)hi);
+                }
+            } else if constexpr (sizeof(XT) == 2) {
+                const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + (a.mid_goff + gsrc[g]) * 16 + 4 * gq;
+                mf[g] = *reinterpret_cast<const i16x4 *>(src);
+            } else {
+                const XT *src = static_cast<const XT *>(a.mid) + row * a.MR + (a.mid_goff + gsrc[g]) * 16 + 4 * gq;
+                mf[g] = *reinterpret_cast<const f32x4 *>(src);
+            }
         }
         YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
         if constexpr (LINE) {
@@ -1068,13 +1112,13 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
 // Two entry points of one body: the second asks the compiler for 4 waves per SIMD (at most
 // 128 VGPRs); it is used where the body fits that budget without spilling (one rank group,
 // bf16 output).
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS = 1>
 __global__ void __launch_bounds__(kThreads) expand_kernel(LoraArgs a) {
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a, (int)blockIdx.x);
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD, NS>(a, (int)blockIdx.x);
 }
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS = 1>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) expand_kernel_w4(LoraArgs a) {
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a, (int)blockIdx.x);
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD, NS>(a, (int)blockIdx.x);
 }
 
 #ifndef LITHE_SHARED_X_NT
@@ -1097,10 +1141,20 @@ void launch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
                        dim3(kThreads), p.lds_s, st, a);
 }
 
-template <typename XT, typename YT, int SRC, int GM, int BOM>
+template <typename XT, typename YT, int SRC, int GM, int BOM, int NS = 1>
 void launch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
     const int64_t bow = (int64_t)p.BO << p.wo_sh;
     dim3 ge((unsigned)(((a.d_out + bow - 1) / bow) * a.n_batch * p.tiles_e));
+    if constexpr (NS != 1) {    // rank % 32 == 0: whole 4-rank fragments
+        if constexpr (GM == 1 && sizeof(YT) == 2) {
+            if (a.accumulate) hipLaunchKernelGGL((expand_kernel_w4<XT, YT, SRC, GM, BOM, true, true, NS>), ge, dim3(kThreads), p.lds_e, st, a);
+            else hipLaunchKernelGGL((expand_kernel_w4<XT, YT, SRC, GM, BOM, false, true, NS>), ge, dim3(kThreads), p.lds_e, st, a);
+        } else {
+            if (a.accumulate) hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, true, true, NS>), ge, dim3(kThreads), p.lds_e, st, a);
+            else hipLaunchKernelGGL((expand_kernel<XT, YT, SRC, GM, BOM, false, true, NS>), ge, dim3(kThreads), p.lds_e, st, a);
+        }
+        return;
+    }
     const bool quad = (a.rank & 3) == 0;
     if constexpr (GM == 1 && sizeof(YT) == 2) {
         if (quad) {
@@ -1169,21 +1223,21 @@ __global__ void __launch_bounds__(kThreads) shrink_group_kernel(GroupArgs g) {
     else shrink_body<XT, SRC, GM, U, false>(a, bid - g.begin[j], g.job[j].a_goff);
 }
 
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS>
 __device__ __forceinline__ void expand_group_body(const GroupArgs &g) {
     const int bid = (int)blockIdx.x;
     const int j = group_job(g, bid);
     LoraArgs a = g.a;
     apply_job(a, g.job[j]);
-    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(a, bid - g.begin[j]);
+    expand_body<XT, YT, SRC, GM, BOM, ACC, QUAD, NS>(a, bid - g.begin[j]);
 }
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS = 1>
 __global__ void __launch_bounds__(kThreads) expand_group_kernel(GroupArgs g) {
-    expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(g);
+    expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD, NS>(g);
 }
-template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD>
+template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS = 1>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) expand_group_kernel_w4(GroupArgs g) {
-    expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD>(g);
+    expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD, NS>(g);
 }
 
 template <typename XT, int SRC, int GM>
@@ -1191,10 +1245,20 @@ void launch_shrink_group(const GroupArgs &g, unsigned grid, size_t lds, hipStrea
     hipLaunchKernelGGL((shrink_group_kernel<XT, SRC, GM, kShrinkU>), dim3(grid), dim3(kThreads), lds, st, g);
 }
 
-template <typename XT, typename YT, int SRC, int GM, int BOM>
+template <typename XT, typename YT, int SRC, int GM, int BOM, int NS = 1>
 void launch_expand_group(const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
-    const bool quad = (g.a.rank & 3) == 0;
     const dim3 ge(grid);
+    if constexpr (NS != 1) {    // rank % 32 == 0: whole 4-rank fragments
+        if constexpr (GM == 1 && sizeof(YT) == 2) {
+            if (g.a.accumulate) hipLaunchKernelGGL((expand_group_kernel_w4<XT, YT, SRC, GM, BOM, true, true, NS>), ge, dim3(kThreads), lds, st, g);
+            else hipLaunchKernelGGL((expand_group_kernel_w4<XT, YT, SRC, GM, BOM, false, true, NS>), ge, dim3(kThreads), lds, st, g);
+        } else {
+            if (g.a.accumulate) hipLaunchKernelGGL((expand_group_kernel<XT, YT, SRC, GM, BOM, true, true, NS>), ge, dim3(kThreads), lds, st, g);
+            else hipLaunchKernelGGL((expand_group_kernel<XT, YT, SRC, GM, BOM, false, true, NS>), ge, dim3(kThreads), lds, st, g);
+        }
+        return;
+    }
+    const bool quad = (g.a.rank & 3) == 0;
     if constexpr (GM == 1 && sizeof(YT) == 2) {
         if (quad) {
             if (g.a.accumulate)
@@ -1224,9 +1288,20 @@ void dispatch_shrink_group(int GM, const GroupArgs &g, unsigned grid, size_t lds
     }
 }
 
-// BOM as in dispatch_expand (bf16 activations).
+// BOM as in dispatch_expand (bf16 activations); GM counts effective groups of NS rank groups.
 template <typename XT, typename YT, int SRC>
-void dispatch_expand_group(int GM, int BOM, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+void dispatch_expand_group(int GM, int BOM, int NS, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+    if (NS == 4) {
+        if (GM == 1) launch_expand_group<XT, YT, SRC, 1, 256, 4>(g, grid, lds, st);
+        else launch_expand_group<XT, YT, SRC, 2, 256, 4>(g, grid, lds, st);
+        return;
+    }
+    if (NS == 2) {
+        if (GM == 1) launch_expand_group<XT, YT, SRC, 1, 256, 2>(g, grid, lds, st);
+        else if (GM == 2) launch_expand_group<XT, YT, SRC, 2, 256, 2>(g, grid, lds, st);
+        else launch_expand_group<XT, YT, SRC, 4, 128, 2>(g, grid, lds, st);
+        return;
+    }
     switch (GM) {
         case 1:
             if (BOM == 256) launch_expand_group<XT, YT, SRC, 1, 256>(g, grid, lds, st);
@@ -1253,7 +1328,20 @@ void dispatch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
 template <typename XT, typename YT, int SRC>
 void dispatch_expand(const Plan &p, const LoraArgs &a, hipStream_t st) {
     constexpr bool bf = sizeof(XT) == 2;
-    switch (p.GM) {
+    if constexpr (bf && SRC != SRC_DENSE) {
+        if (p.NS == 4) {
+            if (p.GE == 1) launch_expand<XT, YT, SRC, 1, 256, 4>(p, a, st);
+            else launch_expand<XT, YT, SRC, 2, 256, 4>(p, a, st);
+            return;
+        }
+        if (p.NS == 2) {
+            if (p.GE == 1) launch_expand<XT, YT, SRC, 1, 256, 2>(p, a, st);
+            else if (p.GE == 2) launch_expand<XT, YT, SRC, 2, 256, 2>(p, a, st);
+            else launch_expand<XT, YT, SRC, 4, 128, 2>(p, a, st);
+            return;
+        }
+    }
+    switch (p.GE) {
         case 1:
             if (bf && p.BOM == 256) launch_expand<XT, YT, SRC, 1, 256>(p, a, st);
             else launch_expand<XT, YT, SRC, 1, 128>(p, a, st);
@@ -1277,7 +1365,7 @@ void launch_expand_f32_f32(const Plan &p, const LoraArgs &a, int src, hipStream_
 // Grouped launches (bf16 activations and outputs, packed 3-level factors); false if the call has
 // no grouped kernel (the caller then launches job by job).
 bool launch_shrink_group_bf16(int GM, const GroupArgs &g, unsigned grid, size_t lds, int src, hipStream_t st);
-bool launch_expand_group_bf16_bf16(int GM, int BOM, const GroupArgs &g, unsigned grid, size_t lds, int src,
+bool launch_expand_group_bf16_bf16(int GM, int BOM, int NS, const GroupArgs &g, unsigned grid, size_t lds, int src,
                                    hipStream_t st);
 
 }  // namespace lithe

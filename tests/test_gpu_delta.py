@@ -41,7 +41,8 @@ def _truth(x, ia, ib, assign, R, d_in, d_out):
 
 
 @pytest.mark.parametrize("seq,d_in,d_out,r", [(256, 3072, 3072, 16), (50, 128, 192, 16), (1, 256, 384, 4),
-                                              (77, 512, 640, 8), (130, 12288, 256, 16)])
+                                              (77, 512, 640, 8), (130, 12288, 256, 16), (64, 512, 640, 64),
+                                              (33, 256, 100, 32), (20, 128, 200, 128), (50, 384, 264, 96)])
 def test_shared_delta_matches_oracle(seq, d_in, d_out, r):
     ads = [random_adapter([("l", d_in, d_out)], rank=r, seed=s) for s in range(3)]
     ia, ib = _stack(ads, "l", "A"), _stack(ads, "l", "B")
@@ -74,6 +75,30 @@ def test_shared_delta_scaling_and_fp32_out():
         got = shared_codebook_lora_delta(*args, scaling, out_dtype=out_dtype)
         want = odelta.shared_delta(to_np(x), ia, opa, ib, opb, assign, 16, 384, scaling, "bf16", od)
         assert rel(to_np(got), want) < REL_BF16, (scaling, out_dtype)
+
+
+@pytest.mark.parametrize("r,d_out", [(32, 264), (64, 640), (128, 200), (96, 100)])
+def test_rank_collapse_matches_per_group_sums(monkeypatch, r, d_out):
+    """Ranks that are multiples of 32 sum the mid values of the rank groups sharing a factor block
+    before the expand's MFMA (the hi / lo bf16 split of the sum); LITHE_EXPAND_NS=1 runs one MFMA
+    per rank group instead. fp32 outputs (no final rounding) agree to 2e-5 relative (fp32
+    accumulation order and the 2^-17 split bound), and both match the oracle."""
+    ads = [random_adapter([("l", 256, d_out)], rank=r, seed=40 + s) for s in range(3)]
+    ia, ib = _stack(ads, "l", "A"), _stack(ads, "l", "B")
+    x = (torch.randn(3, 45, 256, generator=torch.Generator().manual_seed(r)) * 0.5).bfloat16()
+    assign = [2, 1, 0]
+    pa, pb = (p.cuda() for p in lithe_amd.twin_pools())
+    args = (x.cuda(), torch.from_numpy(ia).cuda(), pa, torch.from_numpy(ib).cuda(), pb,
+            torch.tensor(assign, device="cuda", dtype=torch.int32), r, d_out, 0.5)
+    got = shared_codebook_lora_delta(*args, out_dtype=torch.float32)
+    monkeypatch.setenv("LITHE_EXPAND_NS", "1")
+    ref = shared_codebook_lora_delta(*args, out_dtype=torch.float32)
+    err = rel(to_np(got), to_np(ref))
+    opa, opb = ocb.twin_pools()
+    want = odelta.shared_delta(to_np(x), ia, opa, ib, opb, assign, r, d_out, 0.5, "bf16", "fp32")
+    err_o = rel(to_np(got), want)
+    print(f"rank {r} d_out {d_out}: collapsed vs per-group {err:.2e}, vs oracle {err_o:.2e}")
+    assert err < 2e-5 and err_o < REL_BF16
 
 
 def test_shared_delta_fp32_activations():

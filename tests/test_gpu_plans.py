@@ -7,6 +7,8 @@ sizes too large for the oracle, on small shapes with the plan forced through the
   grouping of the K sum, so each is checked against the oracle;
 * the expand with 128- and 256-output waves, 1, 2 or 4 waves along the outputs of a workgroup and
   1 or 2 sub-tiles: the same sums in the same order, so the outputs are bit-identical to each other;
+  the same at ranks 32 and 64 (rank groups summed per factor block) over 1 / 2 waves and 1 / 2 / 4
+  sub-tiles;
 * d_out not a multiple of 8 (the per-element y path), bf16 and fp32 y;
 * a bf16 y that is not 16-byte aligned (the per-element path at d_out = 3072): bit-identical to
   the same call into an aligned y.
@@ -97,6 +99,45 @@ def test_expand_tiles_bit_identical(bank, monkeypatch, name, d_in, d_out):
     assert workspace_errors() == 0
     want = odelta.index_linear(y0.float().cpu().numpy(), _oracle(ads, name, x, assign, d_out, 1.0), "bf16")
     assert rel(outs[0].float().cpu().numpy() - y0.float().cpu().numpy(), want - y0.float().cpu().numpy()) < 1e-2
+
+
+@pytest.mark.parametrize("rank", [32, 64])
+def test_rank_collapse_tiles_bit_identical(monkeypatch, rank):
+    """Rank 32 / 64 (the expand sums the mid values of 2 / 4 rank groups per factor block): 1 or
+    2 waves along the outputs and 1, 2 or 4 sub-tiles compute the same sums in the same order,
+    bit-identical; the result matches the oracle."""
+    mods = [("mid", 512, 640), ("odd", 256, 100)]
+    ads = [random_adapter(mods, rank=rank, seed=520 + s) for s in range(3)]
+    bk, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bk.add(w)
+    pools = (bk.pool_a.bfloat16(), bk.pool_b.bfloat16())
+    g = torch.Generator(device="cuda").manual_seed(rank)
+    for name, d_in, d_out in mods:
+        _, _, sb, a_off, b_off = bk.layout.module(name)
+        x = torch.randn(3, 150, d_in, device="cuda", generator=g).bfloat16()
+        y0 = torch.randn(3, 150, d_out, device="cuda", generator=g).bfloat16()
+        assign = torch.tensor([2, 0, 1], dtype=torch.int32, device="cuda")
+        outs = []
+        for wo in (1, 2):
+            for subs in (1, 2, 4):
+                monkeypatch.setenv("LITHE_EXPAND_WO", str(wo))
+                monkeypatch.setenv("LITHE_EXPAND_SUBS", str(subs))
+                y = y0.clone()
+                packed_lora_delta(x, bk.words, a_off, b_off, 3, pools, assign, rank, sb[0], 0.5, out=y,
+                                  accumulate=True)
+                outs.append(y)
+        for y in outs[1:]:
+            assert torch.equal(y, outs[0]), name
+        assert workspace_errors() == 0
+        ia = np.stack([a.indices[name]["A"] for a in ads]).astype(np.int64)
+        ib = np.stack([a.indices[name]["B"] for a in ads]).astype(np.int64)
+        opa, opb = ocb.twin_pools()
+        want = odelta.shared_delta(x.float().cpu().numpy(), ia, opa, ib, opb, assign.tolist(), rank, d_out, 0.5,
+                                   "bf16", "bf16")
+        y0n = y0.float().cpu().numpy()
+        want = odelta.index_linear(y0n, want, "bf16")
+        assert rel(outs[0].float().cpu().numpy() - y0n, want - y0n) < 1e-2, name
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])

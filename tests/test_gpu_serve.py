@@ -159,11 +159,13 @@ def test_lithe_linear_inference():
     assert torch.equal(b_rec, bh)
 
 
-@pytest.mark.parametrize("n_routes,rank,d_out", [(2, 16, 200), (6, 16, 200), (8, 16, 328), (2, 32, 264), (5, 8, 96)])
+@pytest.mark.parametrize("n_routes,rank,d_out", [(2, 16, 200), (6, 16, 200), (8, 16, 328), (2, 32, 264), (5, 8, 96),
+                                                 (3, 32, 200), (4, 32, 264), (2, 64, 136)])
 def test_serve_bf16_rank_group_tiles(n_routes, rank, d_out):
     """bf16 mixtures over 2..8 rank groups: every output-tile width of the expand (256, 128
     and 64 outputs), partial last tiles, a ragged token count and a sample with one route
-    entry fewer than the others (an empty rank group)."""
+    entry fewer than the others (an empty rank group). Ranks 32 and 64 sum the rank groups of a
+    route before the expand's MFMA (2 to 4 such sums per token, one of them empty for 3 routes)."""
     rng = np.random.default_rng(n_routes * 100 + rank)
     n_ad = n_routes + 1
     routes = []
