@@ -98,7 +98,7 @@ class Workload:
         from lithe_amd.kernels import PackedBank, PackedLayout
         from lithe_amd.kernels.prepared import (group_workspace_bytes, prepare_dense, prepare_packed,
                                                 prepare_packed_group, prepare_packed_shared_x, shared_workspace,
-                                                workspace_bytes)
+                                                shared_x_workspace_bytes, workspace_bytes)
 
         self.name, self.mods, self.batch = name, mods, batch
         dev = torch.device("cuda:0")
@@ -135,7 +135,13 @@ class Workload:
             pool.append(torch.randn(batch, m, d, device=dev, generator=gen).to(torch.bfloat16))
             return pool[-1]
 
-        need = max(workspace_bytes((batch, m, di), do, rank, 3 if qkv else 1, torch.bfloat16) for _, di, do, m in mods)
+        # per-call workspace (grouped workloads size theirs per group below; a q / k / v call of the
+        # per-call path holds the three modules' intermediates)
+        need = 0 if grouped else max(workspace_bytes((batch, m, di), do, rank, 1, torch.bfloat16)
+                                     for _, di, do, m in mods)
+        if qkv and not grouped:
+            need = max([need] + [shared_x_workspace_bytes((batch, m, di), [do] * 3, rank, 1, torch.bfloat16)
+                                 for _, di, do, m in mods])
         groups = flux_groups(mods) if grouped else []
         for gi in groups:
             keys = [_SHARED_INPUT.get(_split(mods[i][0])[1], str(i)) if qkv else str(i) for i in gi]

@@ -44,20 +44,34 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     const int64_t rows = n_batch * seq;
     const int target = env_int("LITHE_TARGET_WAVES", 2048);
 
-    // shrink: one wave per 16 tokens x (K / ks); ks grows until there are enough waves.
+    // shrink token groups per wave: with several rank groups (bf16, packed or indexed factors)
+    // each wave takes two 16-token groups, which share its A fragment reads and the workgroup's
+    // A decode. LITHE_SHRINK_TW=1 / 2 overrides.
+    p.tw = (xbytes == 2 && !dense && p.GMs >= 2) ? 2 : 1;
+    if (const char *v = getenv("LITHE_SHRINK_TW")) p.tw = (atoi(v) == 2 && xbytes == 2 && !dense && p.GMs >= 2) ? 2 : 1;
+
+    // shrink: one wave per 16 tw tokens x (K / ks); ks grows until there are enough waves.
     const int64_t groups = ctx ? ctx->groups : n_batch * ((seq + 15) / 16);
     int ks = 1;
     // long K: shorter per-wave streams; with 4 or 8 rank groups a 4-way split costs more in
     // LDS reads than it gains (measured on the q/k/v shared-input shapes)
     const int ks_max = p.GM >= 4 ? 2 : 4;
-    while (ks < ks_max && (groups * ks < target || d_in / ks > 6144)) ks *= 2;
+    if (p.tw == 1) {
+        while (ks < ks_max && (groups * ks < target || d_in / ks > 6144)) ks *= 2;
+    } else {
+        // Two token groups per wave: a K split halves the tokens that share each A piece; grouped
+        // FLUX sweeps at ranks 32 / 48 / 64 / 96 / 128 ran 58.7 / 79.1 / 64.0 / 114.6 / 86.0 ms
+        // with no split (the 12,288-input projections included) against 60.2 / 82.4 / 72.0 /
+        // 135.2 / 107.4 with the one-group rule. Split only below 1,024 waves.
+        while (ks < ks_max && groups * ks / 2 < target / 2) ks *= 2;
+    }
     if (getenv("LITHE_SHRINK_KS")) {
         const int v = env_int("LITHE_SHRINK_KS", ks);
         ks = v >= 4 ? 4 : v >= 2 ? 2 : 1;
     }
     p.ks = ks;
     const int tgw = kWaves / ks;
-    p.tiles_s = (int)std::max<int64_t>(1, (seq + 16 * tgw - 1) / (16 * tgw));
+    p.tiles_s = (int)std::max<int64_t>(1, (seq + 16 * tgw * p.tw - 1) / (16 * tgw * p.tw));
     // Ring of two LDS regions, each holding the GM*16 factor rows of one K piece of pb blocks:
     // periods (16 values per block; the plan keeps a piece's items within one fill batch) or
     // dense rows (64 values per block). Every piece boundary is a workgroup barrier, so pieces
@@ -85,7 +99,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.region = p.GMs * 16 * p.arow;
     const int64_t npiece = (d_in / kBlock + p.pb - 1) / p.pb;
     p.red_off = kHead + (npiece > 1 ? 2 : 1) * p.region * xbytes;
-    p.stage_off = p.red_off + (ks > 1 ? kWaves * p.GMs * 64 * 16 : 0);
+    p.stage_off = p.red_off + (ks > 1 ? kWaves * p.GMs * 64 * 16 * p.tw : 0);
     p.lds_s = p.stage_off + (size_t)kWaves * std::min(kStageLoads, kShrinkU) * 1024;
 
     // expand rank collapse (bf16 activations, packed or indexed factors): the NS rank groups of an
@@ -684,7 +698,7 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
     hipStream_t st = (hipStream_t)stream;
     const bool grouped = getenv("LITHE_GROUPED_SERIAL") == nullptr;
     if (grouped && launch_shrink_group_bf16_ok(x_dtype, y_dtype, src)) {
-        launch_shrink_group_bf16(ps[0].GMs, gs, (unsigned)grid_s, lds_s, src, st);
+        launch_shrink_group_bf16(ps[0].GMs, ps[0].tw, gs, (unsigned)grid_s, lds_s, src, st);
         launch_expand_group_bf16_bf16(pe[0].GE, pe[0].BOM, pe[0].NS, ge, (unsigned)grid_e, lds_e, src, st);
     } else {
         // job by job through the per-call kernels (other dtypes and factor kinds)

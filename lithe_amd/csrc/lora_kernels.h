@@ -123,6 +123,7 @@ struct LoraArgs {
 struct Plan {
     int G, n_rg, GM, MR;
     int GMs;    // rank groups the shrink is compiled for (GM, or exactly 3 for three groups)
+    int tw;     // shrink: token groups per wave (1 or 2)
     int tiles_s, ks, pb, arow, region, red_off, stage_off;
     size_t lds_s, lds_e;
     int tiles_e, subs_e, BO, BOM, U, nblk_max, estage_off, wo_sh;
@@ -244,7 +245,9 @@ __device__ __forceinline__ void stage_lut(float *lut, const float *v, int tid) {
 // block of each group (kMaxGroups entries in kernel-argument memory; a grouped launch passes its
 // job's table, so its local copy of the arguments is only read at constant offsets and stays in
 // registers).
-template <typename XT, int SRC, int GM, int U, bool XNT>
+// TW token groups per wave (16 tokens each, consecutive): every A fragment read from LDS and
+// every A piece a workgroup decodes serve TW MFMAs / token groups (used with several rank groups).
+template <typename XT, int SRC, int GM, int U, bool XNT, int TW = 1>
 __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const int64_t *goff) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     constexpr bool kBf16 = sizeof(XT) == 2;
@@ -279,9 +282,7 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     if (tile >= (int)a.n_batch * a.tiles_s) return;    // padding (an XCD round, a grouped call): before any barrier
     const int64_t b = tile / a.tiles_s;
     const int mt = tile % a.tiles_s;
-    const int64_t m = ((int64_t)mt * tgw + tgi) * 16 + r16;
-    const bool valid = m < a.seq;
-    const int64_t row = b * a.seq + (valid ? m : a.seq - 1);
+    const int64_t tg0 = ((int64_t)mt * tgw + tgi) * TW;    // first token group of this wave
 
     float *lut = reinterpret_cast<float *>(smem);
     XT *ring = reinterpret_cast<XT *>(smem + kHead);
@@ -471,34 +472,39 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
     // one wave complete in order).
     static_assert(U % 2 == 0, "x loads move pairs of k-steps");
     const int lr = lane >> 3, lc = lane & 7;
-    const XT *lrow[2];
+    const XT *lrow[TW][2];
 #pragma unroll
-    for (int eta = 0; eta < 2; ++eta) {
-        const int64_t lm = ((int64_t)mt * tgw + tgi) * 16 + 8 * eta + lr;
-        lrow[eta] = static_cast<const XT *>(a.x) + (b * a.seq + (lm < a.seq ? lm : a.seq - 1)) * a.d_in +
-                    (lc & 3) * EV;
-    }
+    for (int tw = 0; tw < TW; ++tw)
+#pragma unroll
+        for (int eta = 0; eta < 2; ++eta) {
+            const int64_t lm = (tg0 + tw) * 16 + 8 * eta + lr;
+            lrow[tw][eta] = static_cast<const XT *>(a.x) + (b * a.seq + (lm < a.seq ? lm : a.seq - 1)) * a.d_in +
+                            (lc & 3) * EV;
+        }
     const XT *dummy = static_cast<const XT *>(a.x);
     constexpr int SL = kStageLoads < U ? kStageLoads : U;   // loads staged at a time
     char *stage = smem + a.stage_off + wave * (SL * 1024);
     struct Batch {
-        XV x[U];
+        XV x[TW][U];
     };
     auto load_batch = [&](Batch &bt, const Desc &d) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int st = 2 * (j >> 1) + (lc >> 2);    // step of this lane's chunk inside the batch
-            bt.x[j] = stream_load<XV, XNT>(
-                reinterpret_cast<const XV *>(st < d.n ? lrow[j & 1] + (int64_t)KSTEP * (d.s0 + st) : dummy));
-        }
+        for (int tw = 0; tw < TW; ++tw)
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int st = 2 * (j >> 1) + (lc >> 2);    // step of this lane's chunk inside the batch
+                bt.x[tw][j] = stream_load<XV, XNT>(
+                    reinterpret_cast<const XV *>(st < d.n ? lrow[tw][j & 1] + (int64_t)KSTEP * (d.s0 + st) : dummy));
+            }
     };
-    // loads [m SL, (m + 1) SL) of a batch (steps of the same range) pass through the stage together
-    auto stage_batch = [&](const Batch &bt, int m) __attribute__((always_inline)) {
+    // loads [m SL, (m + 1) SL) of token group tw of a batch (steps of the same range) pass through
+    // the stage together
+    auto stage_batch = [&](const Batch &bt, int tw, int m) __attribute__((always_inline)) {
         wave_lds_sync();    // the other lanes have read the stage's previous contents
 #pragma unroll
         for (int j = m * SL; j < (m + 1) * SL; ++j) {
             const int t = 8 * (j & 1) + lr;
-            *reinterpret_cast<XV *>(stage + (((j - m * SL) >> 1) * 128 + 8 * t + (lc ^ (t >> 1))) * 16) = bt.x[j];
+            *reinterpret_cast<XV *>(stage + (((j - m * SL) >> 1) * 128 + 8 * t + (lc ^ (t >> 1))) * 16) = bt.x[tw][j];
         }
         wave_lds_sync();    // every lane's chunks are in the stage before any lane reads them
     };
@@ -506,15 +512,20 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
         const int c = 4 * (u & 1) + gq;
         return *reinterpret_cast<const XV *>(stage + (((u - m * SL) >> 1) * 128 + 8 * r16 + (c ^ (r16 >> 1))) * 16);
     };
-    f32x4 acc[GM];
+    f32x4 acc[TW][GM];
 #pragma unroll
-    for (int g = 0; g < GM; ++g) acc[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tw = 0; tw < TW; ++tw)
+#pragma unroll
+        for (int g = 0; g < GM; ++g) acc[tw][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute_chunk = [&](const Batch &bt, const Desc &d, const XT *reg, int sp, int m) __attribute__((always_inline)) {
-        stage_batch(bt, m);
-        XV xv[SL];
+        XV xv[TW][SL];
 #pragma unroll
-        for (int v = 0; v < SL; ++v)
-            if (m * SL + v < d.n) xv[v] = staged(m * SL + v, m);
+        for (int tw = 0; tw < TW; ++tw) {
+            stage_batch(bt, tw, m);
+#pragma unroll
+            for (int v = 0; v < SL; ++v)
+                if (m * SL + v < d.n) xv[tw][v] = staged(m * SL + v, m);
+        }
         XV av[SL][GM];
 #pragma unroll
         for (int v = 0; v < SL; ++v)
@@ -533,15 +544,17 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
         for (int v = 0; v < SL; ++v) {
             if (m * SL + v >= d.n) break;
 #pragma unroll
-            for (int g = 0; g < GM; ++g) {
-                if constexpr (kBf16) {
-                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[v][g], xv[v], acc[g], 0, 0, 0);
-                } else {
+            for (int g = 0; g < GM; ++g)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[v][g][e], xv[v][e], acc[g], 0, 0, 0);
+                for (int tw = 0; tw < TW; ++tw) {
+                    if constexpr (kBf16) {
+                        acc[tw][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[v][g], xv[tw][v], acc[tw][g], 0, 0, 0);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[tw][g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[v][g][e], xv[tw][v][e], acc[tw][g], 0, 0, 0);
+                    }
                 }
-            }
         }
     };
 
@@ -616,40 +629,50 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
         enter(npiece - 1);    // every wave passes the same npiece - 1 boundaries
     }
 
-    // acc[g][e]: token r16, rank 4*gq + e of group g, summed over this wave's k range
+    // acc[tw][g][e]: token r16 of group tw, rank 4*gq + e of group g, summed over this wave's k range
     if (ks > 1) {
 #pragma unroll
-        for (int g = 0; g < GM; ++g) *reinterpret_cast<f32x4 *>(red + ((wave * GM + g) * 64 + lane) * 4) = acc[g];
+        for (int tw = 0; tw < TW; ++tw)
+#pragma unroll
+            for (int g = 0; g < GM; ++g)
+                *reinterpret_cast<f32x4 *>(red + (((tw * kWaves + wave) * GM + g) * 64 + lane) * 4) = acc[tw][g];
         __syncthreads();
         if (ksi != 0) return;
 #pragma unroll
-        for (int g = 0; g < GM; ++g) {
-            f32x4 sum = *reinterpret_cast<const f32x4 *>(red + ((tgi * GM + g) * 64 + lane) * 4);
-            for (int k2 = 1; k2 < ks; ++k2)
-                sum += *reinterpret_cast<const f32x4 *>(red + (((k2 * tgw + tgi) * GM + g) * 64 + lane) * 4);
-            acc[g] = sum;
-        }
+        for (int tw = 0; tw < TW; ++tw)
+#pragma unroll
+            for (int g = 0; g < GM; ++g) {
+                f32x4 sum = *reinterpret_cast<const f32x4 *>(red + (((tw * kWaves + tgi) * GM + g) * 64 + lane) * 4);
+                for (int k2 = 1; k2 < ks; ++k2)
+                    sum += *reinterpret_cast<const f32x4 *>(red + (((tw * kWaves + k2 * tgw + tgi) * GM + g) * 64 + lane) * 4);
+                acc[tw][g] = sum;
+            }
     }
-    if (!valid) return;
     const float ms_b = a.mid_scale ? a.mid_scale[b] : 1.0f;
 #pragma unroll
-    for (int g = 0; g < GM; ++g) {
-        if (gs[g] < 0) continue;
-        XT *dst = static_cast<XT *>(a.mid) + row * a.MR + (mod * a.G + g) * 16 + 4 * gq;
-        if constexpr (kBf16) {
-            bf16x4 o;
+    for (int tw = 0; tw < TW; ++tw) {
+        const int64_t m = (tg0 + tw) * 16 + r16;
+        if (m >= a.seq) break;    // later groups are further out
+        const int64_t row = b * a.seq + m;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (__bf16)(acc[g][e] * ms_b);
-            *reinterpret_cast<bf16x4 *>(dst) = o;
-        } else {
-            *reinterpret_cast<f32x4 *>(dst) = acc[g] * ms_b;
+        for (int g = 0; g < GM; ++g) {
+            if (gs[g] < 0) continue;
+            XT *dst = static_cast<XT *>(a.mid) + row * a.MR + (mod * a.G + g) * 16 + 4 * gq;
+            if constexpr (kBf16) {
+                bf16x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = (__bf16)(acc[tw][g][e] * ms_b);
+                *reinterpret_cast<bf16x4 *>(dst) = o;
+            } else {
+                *reinterpret_cast<f32x4 *>(dst) = acc[tw][g] * ms_b;
+            }
         }
     }
 }
 
-template <typename XT, int SRC, int GM, int U, bool XNT>
+template <typename XT, int SRC, int GM, int U, bool XNT, int TW = 1>
 __global__ void __launch_bounds__(kThreads) shrink_kernel(LoraArgs a) {
-    shrink_body<XT, SRC, GM, U, XNT>(a, (int)blockIdx.x, a.a_goff);
+    shrink_body<XT, SRC, GM, U, XNT, TW>(a, (int)blockIdx.x, a.a_goff);
 }
 
 // ============================================================================ expand
@@ -1125,17 +1148,20 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
 #define LITHE_SHARED_X_NT 0
 #endif
 
-template <typename XT, int SRC, int GM>
+// U of a shrink with TW token groups per wave: the x registers of a batch stay at kShrinkU loads
+template <int TW> constexpr int shrink_u() { return kShrinkU / TW >= 2 ? kShrinkU / TW : 2; }
+
+template <typename XT, int SRC, int GM, int TW = 1>
 void launch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
     if constexpr (SRC != SRC_DENSE && !LITHE_SHARED_X_NT) {
         if (a.n_mod_wg > 1) {    // replicated shared-input shrink: x stays in L2 for the other modules
-            hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU, false>),
+            hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, shrink_u<TW>(), false, TW>),
                                dim3((unsigned)((a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg)), dim3(kThreads),
                                p.lds_s, st, a);
             return;
         }
     }
-    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, kShrinkU, true>),
+    hipLaunchKernelGGL((shrink_kernel<XT, SRC, GM, shrink_u<TW>(), true, TW>),
                        dim3((unsigned)(a.n_mod_wg > 1 ? (a.n_batch * p.tiles_s + 7) / 8 * 8 * a.n_mod_wg
                                                       : a.n_batch * p.tiles_s)),
                        dim3(kThreads), p.lds_s, st, a);
@@ -1213,14 +1239,14 @@ __host__ __device__ __forceinline__ void apply_job(LoraArgs &a, const GroupJob &
 
 // The x loads of a job take the non-temporal hint unless the job is a replicated shared input
 // (its modules' workgroups read each x line from L2); the choice is uniform per workgroup.
-template <typename XT, int SRC, int GM, int U>
+template <typename XT, int SRC, int GM, int U, int TW = 1>
 __global__ void __launch_bounds__(kThreads) shrink_group_kernel(GroupArgs g) {
     const int bid = (int)blockIdx.x;
     const int j = group_job(g, bid);
     LoraArgs a = g.a;
     apply_job(a, g.job[j]);
-    if (g.job[j].xnt) shrink_body<XT, SRC, GM, U, true>(a, bid - g.begin[j], g.job[j].a_goff);
-    else shrink_body<XT, SRC, GM, U, false>(a, bid - g.begin[j], g.job[j].a_goff);
+    if (g.job[j].xnt) shrink_body<XT, SRC, GM, U, true, TW>(a, bid - g.begin[j], g.job[j].a_goff);
+    else shrink_body<XT, SRC, GM, U, false, TW>(a, bid - g.begin[j], g.job[j].a_goff);
 }
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, bool ACC, bool QUAD, int NS>
@@ -1240,9 +1266,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     expand_group_body<XT, YT, SRC, GM, BOM, ACC, QUAD, NS>(g);
 }
 
-template <typename XT, int SRC, int GM>
+template <typename XT, int SRC, int GM, int TW = 1>
 void launch_shrink_group(const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((shrink_group_kernel<XT, SRC, GM, kShrinkU>), dim3(grid), dim3(kThreads), lds, st, g);
+    hipLaunchKernelGGL((shrink_group_kernel<XT, SRC, GM, shrink_u<TW>(), TW>), dim3(grid), dim3(kThreads), lds, st, g);
 }
 
 template <typename XT, typename YT, int SRC, int GM, int BOM, int NS = 1>
@@ -1277,8 +1303,18 @@ void launch_expand_group(const GroupArgs &g, unsigned grid, size_t lds, hipStrea
     }
 }
 
+// TW: token groups per wave (2 only with several rank groups).
 template <typename XT, int SRC>
-void dispatch_shrink_group(int GM, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+void dispatch_shrink_group(int GM, int TW, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
+    if (TW == 2) {
+        switch (GM) {
+            case 2: launch_shrink_group<XT, SRC, 2, 2>(g, grid, lds, st); break;
+            case 3: launch_shrink_group<XT, SRC, 3, 2>(g, grid, lds, st); break;
+            case 4: launch_shrink_group<XT, SRC, 4, 2>(g, grid, lds, st); break;
+            default: launch_shrink_group<XT, SRC, 8, 2>(g, grid, lds, st); break;
+        }
+        return;
+    }
     switch (GM) {
         case 1: launch_shrink_group<XT, SRC, 1>(g, grid, lds, st); break;
         case 2: launch_shrink_group<XT, SRC, 2>(g, grid, lds, st); break;
@@ -1315,6 +1351,17 @@ void dispatch_expand_group(int GM, int BOM, int NS, const GroupArgs &g, unsigned
 
 template <typename XT, int SRC>
 void dispatch_shrink(const Plan &p, const LoraArgs &a, hipStream_t st) {
+    if constexpr (SRC != SRC_DENSE && sizeof(XT) == 2) {
+        if (p.tw == 2) {
+            switch (p.GMs) {
+                case 2: launch_shrink<XT, SRC, 2, 2>(p, a, st); break;
+                case 3: launch_shrink<XT, SRC, 3, 2>(p, a, st); break;
+                case 4: launch_shrink<XT, SRC, 4, 2>(p, a, st); break;
+                default: launch_shrink<XT, SRC, 8, 2>(p, a, st); break;
+            }
+            return;
+        }
+    }
     switch (p.GMs) {
         case 1: launch_shrink<XT, SRC, 1>(p, a, st); break;
         case 2: launch_shrink<XT, SRC, 2>(p, a, st); break;
@@ -1364,7 +1411,7 @@ void launch_expand_f32_bf16(const Plan &p, const LoraArgs &a, int src, hipStream
 void launch_expand_f32_f32(const Plan &p, const LoraArgs &a, int src, hipStream_t st);
 // Grouped launches (bf16 activations and outputs, packed 3-level factors); false if the call has
 // no grouped kernel (the caller then launches job by job).
-bool launch_shrink_group_bf16(int GM, const GroupArgs &g, unsigned grid, size_t lds, int src, hipStream_t st);
+bool launch_shrink_group_bf16(int GM, int TW, const GroupArgs &g, unsigned grid, size_t lds, int src, hipStream_t st);
 bool launch_expand_group_bf16_bf16(int GM, int BOM, int NS, const GroupArgs &g, unsigned grid, size_t lds, int src,
                                    hipStream_t st);
 

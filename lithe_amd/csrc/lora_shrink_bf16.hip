@@ -9,9 +9,9 @@ void launch_shrink_bf16(const Plan &p, const LoraArgs &a, int src, hipStream_t s
     else dispatch_shrink<__bf16, SRC_INDEXED>(p, a, st);
 }
 
-bool launch_shrink_group_bf16(int GM, const GroupArgs &g, unsigned grid, size_t lds, int src, hipStream_t st) {
+bool launch_shrink_group_bf16(int GM, int TW, const GroupArgs &g, unsigned grid, size_t lds, int src, hipStream_t st) {
     if (src != SRC_PACKED) return false;
-    dispatch_shrink_group<__bf16, SRC_PACKED>(GM, g, grid, lds, st);
+    dispatch_shrink_group<__bf16, SRC_PACKED>(GM, TW, g, grid, lds, st);
     return true;
 }
 

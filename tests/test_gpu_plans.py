@@ -1,6 +1,7 @@
 """GPU parity of the delta's launch plans and output paths that the serving shapes reach only at
 sizes too large for the oracle, on small shapes with the plan forced through the plan overrides
-(LITHE_SHRINK_KS, LITHE_EXPAND_BO, LITHE_EXPAND_WO, LITHE_EXPAND_SUBS; the library reads them on every call):
+(LITHE_SHRINK_KS, LITHE_SHRINK_TW, LITHE_EXPAND_BO, LITHE_EXPAND_WO, LITHE_EXPAND_SUBS; the library reads
+them on every call):
 
 * the shrink with each token group's K range on 1, 2 or 4 waves (one rank group): 2 waves is the
   plan of the 12288 -> 3072 projections at 1,536 and 4,096 tokens. Results differ only in the fp32
@@ -9,6 +10,8 @@ sizes too large for the oracle, on small shapes with the plan forced through the
   1 or 2 sub-tiles: the same sums in the same order, so the outputs are bit-identical to each other;
   the same at ranks 32 and 64 (rank groups summed per factor block) over 1 / 2 waves and 1 / 2 / 4
   sub-tiles;
+* the shrink with one or two 16-token groups per wave at 2, 3, 4 and 8 rank groups: bit-identical
+  at each K split;
 * d_out not a multiple of 8 (the per-element y path), bf16 and fp32 y;
 * a bf16 y that is not 16-byte aligned (the per-element path at d_out = 3072): bit-identical to
   the same call into an aligned y.
@@ -138,6 +141,41 @@ def test_rank_collapse_tiles_bit_identical(monkeypatch, rank):
         y0n = y0.float().cpu().numpy()
         want = odelta.index_linear(y0n, want, "bf16")
         assert rel(outs[0].float().cpu().numpy() - y0n, want - y0n) < 1e-2, name
+
+
+@pytest.mark.parametrize("rank", [32, 48, 64, 128])
+def test_shrink_two_token_groups_per_wave(monkeypatch, rank):
+    """With several rank groups each shrink wave takes two 16-token groups (LITHE_SHRINK_TW=2, the
+    default there): per token group the same MFMAs in the same order as one group per wave, so the
+    outputs are bit-identical at a given K split (1, 2 and 4 waves per token group), including a
+    ragged last tile (seq 150 and 7) and ranks of 2, 3, 4 and 8 rank groups."""
+    mods = [("mid", 512, 640), ("long", 1536, 256)]
+    ads = [random_adapter(mods, rank=rank, seed=540 + s) for s in range(3)]
+    bk, words = PackedBank.from_adapters(ads, "cuda")
+    for w in words:
+        bk.add(w)
+    pools = (bk.pool_a.bfloat16(), bk.pool_b.bfloat16())
+    g = torch.Generator(device="cuda").manual_seed(rank + 1)
+    for name, d_in, d_out in mods:
+        _, _, sb, a_off, b_off = bk.layout.module(name)
+        for seq in (150, 7):
+            x = torch.randn(3, seq, d_in, device="cuda", generator=g).bfloat16()
+            assign = torch.tensor([1, 2, 0], dtype=torch.int32, device="cuda")
+            for ks in (1, 2, 4):
+                outs = []
+                for tw in (1, 2):
+                    monkeypatch.setenv("LITHE_SHRINK_KS", str(ks))
+                    monkeypatch.setenv("LITHE_SHRINK_TW", str(tw))
+                    outs.append(packed_lora_delta(x, bk.words, a_off, b_off, 3, pools, assign, rank, sb[0], 0.5,
+                                                  out_dtype=torch.float32))
+                assert torch.equal(outs[0], outs[1]), (name, seq, ks)
+            assert workspace_errors() == 0
+            ia = np.stack([a.indices[name]["A"] for a in ads]).astype(np.int64)
+            ib = np.stack([a.indices[name]["B"] for a in ads]).astype(np.int64)
+            opa, opb = ocb.twin_pools()
+            want = odelta.shared_delta(x.float().cpu().numpy(), ia, opa, ib, opb, assign.tolist(), rank, d_out,
+                                       0.5, "bf16", "fp32")
+            assert rel(outs[1].cpu().numpy(), want) < REL_BF16, (name, seq)
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
