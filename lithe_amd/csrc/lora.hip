@@ -146,11 +146,13 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     // output) grows with the groups, its y tile (64 bytes per output and sub-tile) does not, so
     // more tokens per workgroup amortize it: the tile ratio is G / 8. Grouped FLUX sweeps (bf16,
     // packed, rank collapse): rank 32 63.3 -> 60.6 ms and rank 64 83.0 -> 73.9 ms with 2 sub-tiles
-    // (4: slower), rank 128 142.1 -> 127.5 ms with 4. Without the collapse (one MFMA per rank
-    // group) rank 32 was best at 2 (72.2 -> 60.8 ms), rank 64 at 4 to 8 (130.6 -> 83.3 / 80.7 ms).
+    // (4: slower), rank 128 142.1 -> 127.5 ms with 4 and (with the two-token-group shrink)
+    // 86.2 -> 81.8 ms with 8 rather than 4. Without the collapse (one MFMA per rank group) rank 32
+    // was best at 2 (72.2 -> 60.8 ms), rank 64 at 4 to 8 (130.6 -> 83.3 / 80.7 ms).
+    // A grouped launch's grid is the sum of its jobs: its short (512-token) jobs take the rule too.
     if (p.G >= 2) {
-        const int sg = (p.G >= 8 || (p.G >= 4 && p.NS == 1)) ? 4 : 2;
-        if (base_wgs >= (int64_t)sg * 1024) subs = std::max(subs, sg);
+        const int sg = p.G >= 8 ? 8 : (p.G >= 4 && p.NS == 1) ? 4 : 2;
+        if (ctx || base_wgs >= (int64_t)sg * 1024) subs = std::max(subs, sg);
     }
     if (getenv("LITHE_EXPAND_SUBS")) subs = env_int("LITHE_EXPAND_SUBS", subs);
     p.subs_e = subs;

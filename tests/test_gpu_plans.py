@@ -8,8 +8,8 @@ them on every call):
   grouping of the K sum, so each is checked against the oracle;
 * the expand with 128- and 256-output waves, 1, 2 or 4 waves along the outputs of a workgroup and
   1 or 2 sub-tiles: the same sums in the same order, so the outputs are bit-identical to each other;
-  the same at ranks 32 and 64 (rank groups summed per factor block) over 1 / 2 waves and 1 / 2 / 4
-  sub-tiles;
+  the same at ranks 32, 64 and 128 (rank groups summed per factor block) over 1 / 2 waves and
+  1 / 2 / 4 / 8 sub-tiles;
 * the shrink with one or two 16-token groups per wave at 2, 3, 4 and 8 rank groups: bit-identical
   at each K split;
 * d_out not a multiple of 8 (the per-element y path), bf16 and fp32 y;
@@ -104,11 +104,11 @@ def test_expand_tiles_bit_identical(bank, monkeypatch, name, d_in, d_out):
     assert rel(outs[0].float().cpu().numpy() - y0.float().cpu().numpy(), want - y0.float().cpu().numpy()) < 1e-2
 
 
-@pytest.mark.parametrize("rank", [32, 64])
+@pytest.mark.parametrize("rank", [32, 64, 128])
 def test_rank_collapse_tiles_bit_identical(monkeypatch, rank):
-    """Rank 32 / 64 (the expand sums the mid values of 2 / 4 rank groups per factor block): 1 or
-    2 waves along the outputs and 1, 2 or 4 sub-tiles compute the same sums in the same order,
-    bit-identical; the result matches the oracle."""
+    """Rank 32 / 64 / 128 (the expand sums the mid values of 2 / 4 / 4 rank groups per factor
+    block): 1 or 2 waves along the outputs and 1, 2, 4 or 8 sub-tiles compute the same sums in the
+    same order, bit-identical; the result matches the oracle."""
     mods = [("mid", 512, 640), ("odd", 256, 100)]
     ads = [random_adapter(mods, rank=rank, seed=520 + s) for s in range(3)]
     bk, words = PackedBank.from_adapters(ads, "cuda")
@@ -123,7 +123,7 @@ def test_rank_collapse_tiles_bit_identical(monkeypatch, rank):
         assign = torch.tensor([2, 0, 1], dtype=torch.int32, device="cuda")
         outs = []
         for wo in (1, 2):
-            for subs in (1, 2, 4):
+            for subs in (1, 2, 4, 8):
                 monkeypatch.setenv("LITHE_EXPAND_WO", str(wo))
                 monkeypatch.setenv("LITHE_EXPAND_SUBS", str(subs))
                 y = y0.clone()
