@@ -14,7 +14,7 @@ attention outputs, the two up and the two down projections, a single block's
 q / k / v) run as one grouped call: one shrink and one expand launch per stage,
 114 calls per sweep (``--config flux342``: one call per module).
 
-    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|ffn|hb|hb_modules|decode|ingest|encode] [--rank 16|64]
+    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|ffn|hb|hb_modules|decode|ingest|encode] [--rank R]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
