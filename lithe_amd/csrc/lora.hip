@@ -165,6 +165,8 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
     p.estage_off = (int)((p.lds_e + 15) & ~size_t(15));
     if (ybytes == 2 && p.BOM % 64 == 0)
         p.lds_e = p.estage_off + (size_t)kWaves * 16 * std::min(p.BOM, kExchangeOutputs) * 2;
+    if (kXWave && !dense && ybytes == 2 && p.GE == 1 && p.NS == 1 && p.BOM == 256 && p.BO == 256 && p.wo_sh == 1)    // the cross-wave delta tile
+        p.lds_e = p.estage_off + (size_t)std::max(kXWaveBytes, kWaves * 16 * kExchangeOutputs * 2);
 
     // workspace: [error word | mid]
     p.off_mid = 256;

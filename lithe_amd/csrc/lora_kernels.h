@@ -75,8 +75,13 @@ static_assert(kShrinkU % kStageLoads == 0 && kStageLoads % 2 == 0, "the stage ta
 #ifndef LITHE_LINE_UNITS
 #define LITHE_LINE_UNITS 8     // 16-byte units of one token row per whole-line y access (8, 16, 32)
 #endif
+#ifndef LITHE_EXPAND_XWAVE
+#define LITHE_EXPAND_XWAVE 1   // whole-row y accesses with the delta exchanged across the workgroup's waves
+#endif
 constexpr int kExchangeOutputs = LITHE_EXCHANGE_OUTPUTS;   // outputs per expand LDS exchange (whole-line y)
 constexpr int kLineUnits = LITHE_LINE_UNITS;
+constexpr bool kXWave = LITHE_EXPAND_XWAVE != 0;
+constexpr int kXWaveBytes = 32 * 512 * 2;                  // the workgroup's delta tile: 32 rows x 512 bf16
 static_assert(kLineUnits == 8 || kLineUnits == 16 || kLineUnits == 32, "a y access covers 8, 4 or 2 token rows");
 
 // Factor sources: SRC_PACKED is SRC_INDEXED with both index streams PACKED9 with 3 levels (the
@@ -85,6 +90,13 @@ static_assert(kLineUnits == 8 || kLineUnits == 16 || kLineUnits == 32, "a y acce
 enum { SRC_INDEXED = 1, SRC_DENSE = 2, SRC_PACKED = 3 };
 constexpr int kPackedLevels = 3;
 template <int SRC> constexpr int fixed_levels() { return SRC == SRC_PACKED ? kPackedLevels : 0; }
+// Expand variants with the cross-wave y path: one rank group, 256-output waves, indexed factors
+// (with more groups or the rank collapse the path costs registers: 128 VGPRs and 68 bytes of
+// scratch per lane in the 4-waves-per-SIMD variant, 2 waves per SIMD in the others; dense factors'
+// 16 KB B tile plus the 32 KB delta tile leave 3 workgroups per CU: decoded-mode sweep 60.7 ->
+// 66.9 ms).
+template <int SRC, int GM, int BOM, int NS>
+constexpr bool kXWaveKernel = kXWave && SRC != SRC_DENSE && GM == 1 && BOM == 256 && NS == 1;
 
 struct LoraArgs {
     const void *x;
@@ -1055,6 +1067,58 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             }
         }
     };
+    // Cross-wave y path (kXWaveKernel; bf16 y, 2 waves of 256 outputs along the outputs, 32-token
+    // sub-tiles): wave w reads and writes rows 8 w .. 8 w + 7 of the workgroup's 32 x 512 y tile,
+    // one whole 1 KB row per access; the deltas, computed in the MFMA layout by wave (wt, wq) for
+    // rows 16 wt .. and outputs 256 wq .., pass through a 32 KB LDS tile between two workgroup
+    // barriers. 16-byte unit u of tile row t sits at 64 t + (u ^ (t & 15)): the MFMA-layout writes
+    // (16 rows x 4 units per instruction) and the row reads are free of bank conflicts.
+    // Read-modify-write probes (1 GB of 6 KB / 24 KB rows, 32 x 1 KB workgroup tiles): 6.25 / 6.47
+    // TB/s with 8 whole rows per wave against 5.95-6.11 / 6.24-6.42 with 16 rows x 512 B per wave.
+    // FLUX sweeps (alternating builds, one box): grouped 54.69-54.80 -> 53.94-54.01 ms, per module
+    // 57.55 -> 56.41, hb 62.89 -> 62.05.
+    auto xwave_subtile = [&](int sub, const Frag *mf) __attribute__((always_inline)) {
+        __bf16 *tile = reinterpret_cast<__bf16 *>(smem + a.estage_off);
+        auto tunit = [&](int t, int u) __attribute__((always_inline)) { return tile + (64 * t + (u ^ (t & 15))) * 8; };
+        __bf16 *yb = static_cast<__bf16 *>(a.y);
+        const int64_t m0 = ((int64_t)mt * a.subs_e + sub) * TPS + 8 * wave;
+        const int64_t o8 = obase_wg + 8 * lane;
+        const int64_t oc = std::min<int64_t>(o8, omax);
+        bf16x8 yv[8];
+        if constexpr (ACC) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t m = m0 + i;
+                yv[i] = stream_load<bf16x8, true>(reinterpret_cast<const bf16x8 *>(
+                    yb + (b * a.seq + (m < a.seq ? m : a.seq - 1)) * a.d_out + oc));
+            }
+        }
+        if (sub > 0) __syncthreads();    // every wave has read the previous sub-tile's deltas
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            float vals[8];
+            compute(mf, p, vals);
+            bf16x8 d;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d[e] = (__bf16)(DT<YT>::round(vals[e]) * s_b);
+            *reinterpret_cast<bf16x8 *>(tunit(16 * wt + r16, 32 * wq + 4 * p + gq)) = d;
+        }
+        __syncthreads();                 // the whole tile is written
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const bf16x8 d = *reinterpret_cast<const bf16x8 *>(tunit(8 * wave + i, lane));
+            bf16x8 out;
+            if constexpr (ACC) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) out[e] = (__bf16)((float)yv[i][e] + (float)d[e]);
+            } else {
+                out = d;
+            }
+            const int64_t m = m0 + i;
+            if (m < a.seq && o8 < a.d_out)
+                stream_store<bf16x8, true>(reinterpret_cast<bf16x8 *>(yb + (b * a.seq + m) * a.d_out + o8), out);
+        }
+    };
     for (int sub = 0; sub < a.subs_e; ++sub) {
         // keeps the B fragment reads inside the loop (read from LDS per use, not held in registers)
         asm volatile("" ::: "memory");
@@ -1088,6 +1152,12 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             }
         }
         YT *yr = static_cast<YT *>(a.y) + row * a.d_out;
+        if constexpr (kXWaveKernel<SRC, GM, BOM, NS> && LINE) {
+            if (a.vec_y && a.wo_sh == 1 && a.BO == 256) {
+                xwave_subtile(sub, mf);
+                continue;
+            }
+        }
         if constexpr (LINE) {
             if (a.vec_y) {
                 bf16x8 yv[NJ];
