@@ -79,6 +79,27 @@ def test_codeword_period_16_and_popcount_closed_form():
         assert np.array_equal(t[:, tt], 9 - 2 * pc)
 
 
+@pytest.mark.parametrize("rank,collapses", [(32, True), (64, True), (128, True), (48, False)])
+def test_rank_groups_sharing_a_factor_block_have_equal_columns(rank, collapses):
+    """The expand's rank collapse: B (d_out x r) is the flat factor o * r + j cut into 64-value
+    blocks, each four copies of a 16-value period, so when r is a multiple of 32 the 16-rank groups
+    of an output that fall in one block have equal columns and (sum of their mid values) . P equals
+    mid . B^T. At r = 48 an output's groups straddle blocks: the columns differ."""
+    d_out = 40
+    ad = random_adapter([("l", 64, d_out)], rank=rank, seed=rank)
+    pa, pb = ocb.twin_pools()
+    b = odec.decode(np.asarray(ad.indices["l"]["B"]).astype(np.int64), (d_out, rank), pb).astype(np.float64)
+    ns = 4 if rank % 64 == 0 else 2
+    same = all(np.array_equal(b[:, 16 * (ns * e):16 * (ns * e + 1)], b[:, 16 * (ns * e + q):16 * (ns * e + q + 1)])
+               for e in range(rank // (16 * ns)) for q in range(ns))
+    assert same == collapses
+    if collapses:
+        mid = np.random.default_rng(rank).standard_normal((9, rank))
+        z = mid.reshape(9, rank // (16 * ns), ns, 16).sum(axis=2)                     # the summed fragments
+        p = b.reshape(d_out, rank // (16 * ns), ns, 16)[:, :, 0, :]                    # one period per set
+        np.testing.assert_allclose(np.einsum("tec,oec->to", z, p), mid @ b.T, rtol=1e-12, atol=1e-15)
+
+
 # ------------------------------------------------------------------ packing
 def test_pack_roundtrip_sizes_and_range():
     rng = np.random.default_rng(1)
