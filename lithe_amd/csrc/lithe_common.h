@@ -172,6 +172,31 @@ __device__ __forceinline__ float decode_value(const float *lut /* [levels][10] i
     return v;
 }
 
+// The values at period positions t and t + 8 (t < 8). sign_mask(t + 8) = sign_mask(t) ^ 0x100 and
+// bit 8 of sign_mask(t) is set, so per level popcount((k ^ m_{t+8}) & 511) is the position-t count
+// plus 1 when bit 8 of k is set and minus 1 when it is clear (the count stays in [0, 9]): one table
+// offset per level and index replaces the second xor and popcount. Same table entries, same fp32
+// order as two decode_value calls.
+template <int LV = 0>
+__device__ __forceinline__ void decode_value_pair(const float *lut, int L, const uint32_t k[kMaxLevels], uint32_t m,
+                                                  float &lo, float &hi) {
+    int pc = __builtin_popcount((k[0] ^ m) & kIndexMask);
+    int d = (int)((k[0] >> 8) & 1u) * 2 - 1;
+    lo = lut[pc];
+    hi = lut[pc + d];
+#pragma unroll
+    for (int l = 1; l < kMaxLevels; ++l)
+        if (LV > 0 ? l < LV : l < L) {
+            pc = __builtin_popcount((k[l] ^ m) & kIndexMask);
+            d = (int)((k[l] >> 8) & 1u) * 2 - 1;
+            lo += lut[l * 10 + pc];
+            hi += lut[l * 10 + d + pc];
+        }
+}
+static_assert((sign_mask(0) ^ 0x100u) == sign_mask(8) && (sign_mask(3) ^ 0x100u) == sign_mask(11) &&
+                  (sign_mask(7) ^ 0x100u) == sign_mask(15) && (sign_mask(5) & 0x100u) != 0,
+              "positions t and t + 8 differ in bit 8 of the sign mask only");
+
 // ---------------------------------------------------------------- dtype helpers
 template <typename T> struct DT;
 template <> struct DT<__bf16> {

@@ -396,10 +396,12 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
             const float w = group_weight(gr >> 4);
             float v[16];
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
+            for (int t = 0; t < 8; ++t) {
                 // unconditional lookups, then a select: no branch between the table reads
-                const float d = decode_value<fixed_levels<SRC>()>(lut, a.a_src.levels, k, sign_mask(t)) * w;
-                v[t] = live ? d : 0.0f;
+                float lo, hi;
+                decode_value_pair<fixed_levels<SRC>()>(lut, a.a_src.levels, k, sign_mask(t), lo, hi);
+                v[t] = live ? lo * w : 0.0f;
+                v[t + 8] = live ? hi * w : 0.0f;
             }
             if constexpr (kSplitHalves) {
                 // bf16: the two 8-value halves of a period sit pb units apart in the row
@@ -846,7 +848,8 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
 
     // ---- B tile of this output range into LDS (bp), read from there by every MFMA.
     // Indexed: the 16-value periods of blocks [blk_lo, blk_lo + nblk) of every route entry,
-    // one item per quarter period (4 values), 2 items per thread per batch.
+    // one item per pair of quarter periods (positions 4 q .. 4 q + 3 and 4 q + 8 .. 4 q + 11, decoded
+    // together: decode_value_pair), 2 items per thread per batch.
     // Dense: rows o in [obase_wg, o_end_wg) of every route entry's B, (route, o - obase_wg, rank).
     float *lut = reinterpret_cast<float *>(smem);
     XT *bp = reinterpret_cast<XT *>(smem + kHead);
@@ -855,14 +858,14 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
     const int64_t o_end_wg = std::min<int64_t>(obase_wg + BOW, a.d_out);
     const int64_t o_end = std::min<int64_t>(obase + a.BO, a.d_out);
     if constexpr (SRC != SRC_DENSE) {
-        const int per_route = (int)(((o_end_wg * a.rank + kBlock - 1) >> 6) - blk_lo) * 4;
+        const int per_route = (int)(((o_end_wg * a.rank + kBlock - 1) >> 6) - blk_lo) * 2;
         const int items = a.n_route * per_route;
         RawIdx raw[2];
         // block of item `it` inside the factor; 0 if its route entry is empty
         auto dec_block = [&](int it, int64_t &slot, float &w, float &sc) __attribute__((always_inline)) -> int64_t {
             const int j = a.n_route == 1 ? 0 : it / per_route;
             route_pick(j, slot, w, sc);
-            const int64_t blk = blk_lo + ((it - j * per_route) >> 2);
+            const int64_t blk = blk_lo + ((it - j * per_route) >> 1);
             return slot >= 0 ? blk : 0;
         };
         auto dec_load = [&](int base) __attribute__((always_inline)) {
@@ -882,27 +885,32 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
                 if (it >= items) break;
                 const int j = a.n_route == 1 ? 0 : it / per_route;
                 const int rem = it - j * per_route;
-                const int blk = rem >> 2, qt = rem & 3;
+                const int blk = rem >> 1, qp = rem & 1;
                 int64_t slot;
                 float w, sc;
                 uint32_t k[kMaxLevels];
                 const bool ok = extract_indices<SRC == SRC_PACKED, fixed_levels<SRC>()>(a.b_src, dec_block(it, slot, w, sc), raw[q], k);
                 const bool live = slot >= 0;
                 if (live && !ok) record_error(a.err, kErrIndex);
-                XT *dst = bp + ((int64_t)j * a.nblk_max + blk) * 16 + 4 * qt;
-                float v[4];
+                XT *dst = bp + ((int64_t)j * a.nblk_max + blk) * 16 + 4 * qp;
+                float v[8];    // positions 4 qp + e and 4 qp + 8 + e
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float d = (decode_value<fixed_levels<SRC>()>(lut, a.b_src.levels, k, sign_mask_rt(4 * qt + e)) * sc) * w;
-                    v[e] = live ? d : 0.0f;
+                    float lo, hi;
+                    decode_value_pair<fixed_levels<SRC>()>(lut, a.b_src.levels, k, sign_mask_rt(4 * qp + e), lo, hi);
+                    v[e] = live ? (lo * sc) * w : 0.0f;
+                    v[4 + e] = live ? (hi * sc) * w : 0.0f;
                 }
-                if constexpr (sizeof(XT) == 2) {
-                    bf16x4 pk;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) pk[e] = (__bf16)v[e];
-                    *reinterpret_cast<bf16x4 *>(dst) = pk;
-                } else {
-                    *reinterpret_cast<f32x4 *>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+                for (int h = 0; h < 2; ++h) {
+                    if constexpr (sizeof(XT) == 2) {
+                        bf16x4 pk;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) pk[e] = (__bf16)v[4 * h + e];
+                        *reinterpret_cast<bf16x4 *>(dst + 8 * h) = pk;
+                    } else {
+                        *reinterpret_cast<f32x4 *>(dst + 8 * h) = f32x4{v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                    }
                 }
             }
         };
