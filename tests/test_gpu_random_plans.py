@@ -1,6 +1,7 @@
 """Seeded random sweep of the index-resident delta against the oracle: ranks 16-128 (one to eight
 rank groups; the rank collapse at 32, 64, 96 and 128), per-call and grouped launches of one to three
-modules with their own token counts, bf16 and fp32 outputs, write and accumulate mode, and random
+modules with their own token counts or all reading one x (the shared-input shrink), bf16 and fp32
+outputs, write and accumulate mode, and random
 plan overrides (waves along the outputs, expand sub-tiles, the shrink's K split and token groups
 per wave, the rank collapse off). Every plan computes the same delta up to the fp32 summation
 order, so each case must meet the bf16 tolerance of tests/test_gpu_delta.py (rel-Frobenius 2e-3
@@ -30,6 +31,10 @@ def _case(rng, monkeypatch):
     shapes = [(f"m{m}", int(rng.integers(1, 33)) * 64, int(rng.integers(2, 400)) * 4) for m in range(n_mod)]
     n_ad, batch = int(rng.integers(1, 5)), int(rng.integers(1, 5))
     seqs = [int(rng.integers(1, 300)) for _ in range(n_mod)]
+    share = grouped and n_mod > 1 and bool(rng.integers(0, 2))    # every module reads one x
+    if share:
+        shapes = [(nm, shapes[0][1], do) for nm, _, do in shapes]
+        seqs = [seqs[0]] * n_mod
     out_dt = torch.bfloat16 if rng.integers(0, 3) else torch.float32
     acc, scale = bool(rng.integers(0, 2)), float(rng.choice([1.0, 0.5, 2.0]))
     for k, v in KNOBS.items():
@@ -37,7 +42,7 @@ def _case(rng, monkeypatch):
             monkeypatch.setenv(k, v[int(rng.integers(0, len(v)))])
         else:
             monkeypatch.delenv(k, raising=False)
-    desc = (rank, grouped, shapes, seqs, batch, n_ad, out_dt, acc, scale)
+    desc = (rank, grouped, share, shapes, seqs, batch, n_ad, out_dt, acc, scale)
     ads = [random_adapter(shapes, rank=rank, seed=int(rng.integers(0, 1 << 30))) for _ in range(n_ad)]
     bk, words = PackedBank.from_adapters(ads, "cuda")
     for w in words:
@@ -46,14 +51,16 @@ def _case(rng, monkeypatch):
     assign = torch.tensor(rng.integers(0, n_ad, batch), dtype=torch.int32, device="cuda")
     gen = torch.Generator(device="cuda").manual_seed(int(rng.integers(0, 1 << 30)))
     xs = [torch.randn(batch, s, di, device="cuda", generator=gen).bfloat16() for (_, di, _), s in zip(shapes, seqs)]
+    if share:
+        xs = [xs[0]] * n_mod
     if grouped:
         acc = True
         y0s = [(torch.randn(batch, s, do, device="cuda", generator=gen) if out_dt == torch.bfloat16
                 else torch.zeros(batch, s, do, device="cuda")).to(out_dt) for (_, _, do), s in zip(shapes, seqs)]
         outs = [y.clone() for y in y0s]
         offs = [bk.layout.module(nm)[3:5] for nm, _, _ in shapes]
-        need = group_workspace_bytes([(s, di, do) for (_, di, do), s in zip(shapes, seqs)], list(range(n_mod)),
-                                     batch, rank, 1, torch.bfloat16)
+        need = group_workspace_bytes([(s, di, do) for (_, di, do), s in zip(shapes, seqs)],
+                                     [0] * n_mod if share else list(range(n_mod)), batch, rank, 1, torch.bfloat16)
         prepare_packed_group(xs, outs, bk.words, offs, 3, pools, assign, rank, scale, shared_workspace("cuda", need),
                              accumulate=True)()
     else:
