@@ -6,10 +6,15 @@ plan overrides (waves along the outputs, expand sub-tiles, the shrink's K split 
 per wave, the rank collapse off). Every plan computes the same delta up to the fp32 summation
 order, so each case must meet the bf16 tolerance of tests/test_gpu_delta.py (rel-Frobenius 2e-3
 against the oracle; 1e-2 on the change of an accumulated bf16 output, which includes the rounding
-of y + delta)."""
+of y + delta). A second sweep runs serve.py's mixture routing."""
+import math
+
 import numpy as np
 import pytest
 import torch
+from torch import nn
+
+from lithe_amd import serve
 
 from lithe_amd.kernels import PackedBank, packed_lora_delta, workspace_errors
 from lithe_amd.kernels.prepared import group_workspace_bytes, prepare_packed_group, shared_workspace
@@ -98,3 +103,60 @@ def test_random_plans_match_oracle(monkeypatch, seed):
     rng = np.random.default_rng(seed)
     for _ in range(50):
         _case(rng, monkeypatch)
+
+
+class _One(nn.Module):
+    def __init__(self, d_in, d_out):
+        super().__init__()
+        self.fc = nn.Linear(d_in, d_out)
+
+    def forward(self, x):
+        return self.fc(x)
+
+
+def test_random_mixtures_match_serve_oracle(monkeypatch):
+    """serve.py mixture routing (0 to 8 / ceil(rank / 16) weighted route entries per sample, ranks
+    8-128, bf16 and fp32 activations) under random plan overrides against the oracle's
+    serve_forward: rtol / atol 1e-5 in fp32, rel-Frobenius 2e-3 in bf16 (tests/test_gpu_serve.py)."""
+    rng = np.random.default_rng(21)
+    pa, pb = ocb.twin_pools()
+    for n in range(60):
+        rank = int(rng.choice([8, 16, 32, 48, 64, 128]))
+        n_routes = int(rng.integers(1, max(1, 8 // ((rank + 15) // 16)) + 1))
+        n_ad = n_routes + int(rng.integers(0, 3))
+        d_in = int(rng.integers(1, 25)) * 64
+        d_out = int(rng.integers(2, 300)) * (64 // math.gcd(64, rank))
+        batch, seq = int(rng.integers(1, 5)), int(rng.integers(1, 200))
+        dtype = torch.bfloat16 if rng.integers(0, 3) else torch.float32
+        for k, v in KNOBS.items():
+            if rng.integers(0, 2):
+                monkeypatch.setenv(k, v[int(rng.integers(0, len(v)))])
+            else:
+                monkeypatch.delenv(k, raising=False)
+        routes = []
+        for _ in range(batch):
+            ids = rng.choice(n_ad, int(rng.integers(0, n_routes + 1)), replace=False)
+            w = rng.uniform(0.2, 1.0, len(ids))
+            w = w / max(w.sum(), 1e-6)
+            routes.append([(int(a), float(v)) for a, v in zip(ids, w)])
+        ads = [random_adapter([("fc", d_in, d_out)], rank=rank, seed=int(rng.integers(0, 1 << 30))) for _ in range(n_ad)]
+        for a in ads:
+            a.alpha = float(rng.choice([rank, 2 * rank]))
+        torch.manual_seed(n)
+        model = _One(d_in, d_out).cuda().to(dtype)
+        router, layers = serve.attach_adapters(model, ads)
+        router.set(routes)
+        x = torch.randn(batch, seq, d_in, generator=torch.Generator().manual_seed(n)).to(dtype)
+        with torch.no_grad():
+            base_out = layers["fc"].base(x.cuda()).float().cpu().numpy()
+            y = model(x.cuda()).float().cpu().numpy()
+        ia = np.stack([a.indices["fc"]["A"] for a in ads])
+        ib = np.stack([a.indices["fc"]["B"] for a in ads])
+        scales = np.array([a.alpha / a.rank for a in ads], np.float32)
+        want = odelta.serve_forward(x.float().numpy(), base_out, router.ids.numpy(), router.weights.numpy(), ia, ib,
+                                    scales, pa, pb, rank, "fp32" if dtype == torch.float32 else "bf16")
+        case = (rank, n_routes, d_in, d_out, batch, seq, dtype, routes)
+        if dtype == torch.float32:
+            np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-5, err_msg=str(case))
+        else:
+            assert rel(y, want) < 2e-3, case
