@@ -19,17 +19,19 @@
 // g runs over "rank groups": route entry j of a sample contributes ceil(rank/16) groups of
 // 16 ranks (rank-stacked mixtures, lithe/serve.py:89-96).
 //
-// shrink  v_mfma_f32_16x16x32_bf16 (fp32: 16x16x4 f32), one wave per 16 tokens x K slice.
-//         A-operand = factor rows (lane%16 = rank), B-operand = x^T (lane%16 = token); lane
-//         group q = lane/16 owns k = 8q..8q+7 of each 32-wide step, so every row of x is read
-//         in 64-byte pieces. Loads are software-pipelined two batches deep with no branch
-//         between a load and its use. Waves that split one token group's K range reduce their
-//         fp32 partials through LDS in a fixed order (deterministic).
-// expand  v_mfma_f32_16x16x16_bf16 (fp32: 16x16x4 f32) with the factor B tile as the
-//         A-operand (lane%16 = output row) and mid^T as the B-operand (lane%16 = token).
-//         Output rows are assigned so that each lane ends with 8 consecutive outputs of its
-//         token: y is read-modified-written 16 bytes per lane with the reference's rounding
-//         chain applied in registers, the next sub-tile's loads in flight.
+// shrink  v_mfma_f32_16x16x32_bf16 (fp32: 16x16x4 f32), one wave per 16 tokens x K slice (two
+//         16-token groups per wave with two or more rank groups). A-operand = factor rows
+//         (lane%16 = rank), B-operand = x^T (lane%16 = token); lane group q = lane/16 owns
+//         k = 8q..8q+7 of each 32-wide step. x arrives in whole 128-byte-line non-temporal loads,
+//         software-pipelined two batches deep, and is reshuffled into that layout through a
+//         per-wave LDS stage. Waves that split one token group's K range reduce their fp32
+//         partials through LDS in a fixed order (deterministic).
+// expand  v_mfma_f32_16x16x16_bf16 (fp32: 16x16x4 f32; 16x16x32 on summed rank groups at ranks
+//         that are multiples of 32) with the factor B tile as the A-operand (lane%16 = output
+//         row) and mid^T as the B-operand (lane%16 = token). Each lane ends with 8 consecutive
+//         outputs of its token; the reference's rounding chain is applied in registers and the
+//         deltas pass through LDS so that y is read-modified-written in whole-line non-temporal
+//         accesses (whole 1 KB rows per wave with one rank group).
 #pragma once
 
 #include <stdint.h>
