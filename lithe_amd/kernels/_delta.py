@@ -79,6 +79,9 @@ def routes(slot: torch.Tensor, weight_sqrt: Optional[torch.Tensor] = None,
     return r
 
 
+_need: dict = {}    # workspace bytes per (n_batch, seq, d_in, d_out, rank, n_route, x dtype)
+
+
 def lora_delta(x: torch.Tensor, y: torch.Tensor, *, rank: int, factors: _hip.Factors, route: _hip.Routes,
                accumulate: bool, mid_scale: Optional[torch.Tensor] = None, out_scale: float = 1.0,
                out_scale_vec: Optional[torch.Tensor] = None, keep: tuple = ()) -> torch.Tensor:
@@ -91,8 +94,14 @@ def lora_delta(x: torch.Tensor, y: torch.Tensor, *, rank: int, factors: _hip.Fac
     n_batch, seq, d_in = x.shape
     d_out = y.shape[2]
     xd = _hip.dtype_code(x.dtype)
-    need = lib.lithe_lora_workspace_bytes(n_batch, seq, d_in, d_out, rank, route.n_route, xd)
-    _hip.check(int(need) if need < 0 else 0, "lithe_lora_workspace_bytes")
+    wkey = (n_batch, seq, d_in, d_out, rank, route.n_route, xd)
+    need = _need.get(wkey)
+    if need is None:
+        need = lib.lithe_lora_workspace_bytes(n_batch, seq, d_in, d_out, rank, route.n_route, xd)
+        _hip.check(int(need) if need < 0 else 0, "lithe_lora_workspace_bytes")
+        if len(_need) > 4096:
+            _need.clear()
+        _need[wkey] = need
     ws = _hip.workspace(x.device, int(need))
     rc = lib.lithe_lora_delta(
         _hip.ptr(x), xd, n_batch, seq, d_in, _hip.ptr(y), _hip.dtype_code(y.dtype), d_out,

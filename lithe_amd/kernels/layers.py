@@ -140,6 +140,7 @@ class IndexLoRALinear(nn.Module):
         self.scaling = float(scaling)
         self.assign: Optional[torch.Tensor] = None
         self._bank = None          # (PackedBank, a_off, b_off) for bank-backed layers
+        self._eager = None         # (key, factors, route) of the last eager call
         idx = {}
         for name, t, blocks in (("idx_a", idx_a, -(-self.rank * base.in_features // 64)),
                                 ("idx_b", idx_b, -(-self.d_out * self.rank // 64))):
@@ -198,11 +199,27 @@ class IndexLoRALinear(nn.Module):
         else:
             if assign.shape != (bsz,):
                 raise ValueError(f"assign must be ({bsz},)")
-            slots = assign.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
+            if assign.dtype == torch.int32 and assign.device == x.device and assign.is_contiguous():
+                slots = assign.view(-1, 1)
+            else:
+                slots = assign.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous()
         if not out3.is_contiguous():
             out3 = out3.contiguous()
             out = out3.squeeze(1) if squeeze else out3
-        # through the torch.library ops (lithe_amd/kernels/ops.py): one opaque in-place op for
+        if not torch.compiler.is_compiling():
+            # eager: the operator's body without the dispatcher, with the call descriptors kept
+            # while the factors, tables and slot tensor stay the same (the kernels read the slot
+            # values at launch, so an in-place update of assign needs no new descriptor)
+            src = self._bank[0].words if self._bank is not None else self.idx_a
+            key = (x.dtype, src.data_ptr(), self.idx_b.data_ptr(), _hip.version_of(self.pool_a),
+                   _hip.version_of(self.pool_b), slots.data_ptr(), slots.shape[0])
+            if self._eager is None or self._eager[0] != key:
+                self._eager = (key, self._factors(x.dtype), _delta.routes(slots))
+            _, f, route = self._eager
+            _delta.lora_delta(x3.contiguous(), out3, rank=self.rank, factors=f, route=route, accumulate=True,
+                              out_scale=self.scaling)
+            return out
+        # traced: the torch.library ops (lithe_amd/kernels/ops.py), one opaque in-place op for
         # torch.compile / FX
         if self._bank is not None:
             bank, a_off, b_off = self._bank

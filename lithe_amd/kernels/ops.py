@@ -30,13 +30,28 @@ def _run(x: torch.Tensor, y: torch.Tensor, a_src, b_src, pool_a: torch.Tensor, p
     _delta.lora_delta(x, y, rank=rank, factors=f, route=_delta.routes(slots), accumulate=True, out_scale=scaling)
 
 
+def bank_delta(x: torch.Tensor, y: torch.Tensor, words: torch.Tensor, a_off: int, b_off: int,
+               pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor, rank: int, scaling: float) -> None:
+    """The body of ``lithe_amd::bank_lora_delta_``, called directly in eager mode."""
+    L = int(pool_a.shape[0])
+    _run(x, y, _delta.packed_source(words, L, a_off), _delta.packed_source(words, L, b_off), pool_a, pool_b, slots,
+         rank, scaling)
+
+
+def index_delta(x: torch.Tensor, y: torch.Tensor, idx_a: torch.Tensor, idx_b: torch.Tensor,
+                pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor, rank: int, scaling: float) -> None:
+    """The body of ``lithe_amd::index_lora_delta_``, called directly in eager mode."""
+    L = int(pool_a.shape[0])
+    d_in, d_out = x.shape[-1], y.shape[-1]
+    _run(x, y, _delta.index_source(idx_a, L, rank * d_in // 64), _delta.index_source(idx_b, L, d_out * rank // 64),
+         pool_a, pool_b, slots, rank, scaling)
+
+
 @torch.library.custom_op("lithe_amd::bank_lora_delta_", mutates_args=("y",), device_types="cuda")
 def bank_lora_delta_(x: torch.Tensor, y: torch.Tensor, words: torch.Tensor, a_off: int, b_off: int,
                      pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor, rank: int,
                      scaling: float) -> None:
-    L = int(pool_a.shape[0])
-    _run(x, y, _delta.packed_source(words, L, a_off), _delta.packed_source(words, L, b_off), pool_a, pool_b, slots,
-         rank, scaling)
+    bank_delta(x, y, words, a_off, b_off, pool_a, pool_b, slots, rank, scaling)
 
 
 @bank_lora_delta_.register_fake
@@ -48,10 +63,7 @@ def _bank_lora_delta_fake(x, y, words, a_off, b_off, pool_a, pool_b, slots, rank
 def index_lora_delta_(x: torch.Tensor, y: torch.Tensor, idx_a: torch.Tensor, idx_b: torch.Tensor,
                       pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor, rank: int,
                       scaling: float) -> None:
-    L = int(pool_a.shape[0])
-    d_in, d_out = x.shape[-1], y.shape[-1]
-    _run(x, y, _delta.index_source(idx_a, L, rank * d_in // 64), _delta.index_source(idx_b, L, d_out * rank // 64),
-         pool_a, pool_b, slots, rank, scaling)
+    index_delta(x, y, idx_a, idx_b, pool_a, pool_b, slots, rank, scaling)
 
 
 @index_lora_delta_.register_fake
@@ -59,13 +71,13 @@ def _index_lora_delta_fake(x, y, idx_a, idx_b, pool_a, pool_b, slots, rank, scal
     return None
 
 
-@torch.library.custom_op("lithe_amd::bank_lora_delta_grouped_", mutates_args=("ys",), device_types="cuda")
-def bank_lora_delta_grouped_(xs: List[torch.Tensor], ys: List[torch.Tensor], words: torch.Tensor, a_offs: List[int],
-                             b_offs: List[int], pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor,
-                             rank: int, scales: List[float]) -> None:
+def bank_delta_grouped(xs: List[torch.Tensor], ys: List[torch.Tensor], words: torch.Tensor, a_offs: List[int],
+                       b_offs: List[int], pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor,
+                       rank: int, scales: List[float]) -> None:
     """ys[m] += delta of module m (blocks at a_offs[m] / b_offs[m] of the packed bank) over xs[m],
     every module in one shrink and one expand launch (``lithe_lora_delta_grouped``); modules
-    given the same x tensor share its shrink."""
+    given the same x tensor share its shrink. The body of ``lithe_amd::bank_lora_delta_grouped_``,
+    called directly in eager mode."""
     import ctypes
     from .prepared import group_workspace_bytes
     n = len(xs)
@@ -88,6 +100,13 @@ def bank_lora_delta_grouped_(xs: List[torch.Tensor], ys: List[torch.Tensor], wor
                                               1, rank, ctypes.byref(f), ctypes.byref(route), _hip.ptr(ws), ws.numel(),
                                               _hip.stream_of(xs[0].device))
     _hip.check(rc, "lithe_lora_delta_grouped")
+
+
+@torch.library.custom_op("lithe_amd::bank_lora_delta_grouped_", mutates_args=("ys",), device_types="cuda")
+def bank_lora_delta_grouped_(xs: List[torch.Tensor], ys: List[torch.Tensor], words: torch.Tensor, a_offs: List[int],
+                             b_offs: List[int], pool_a: torch.Tensor, pool_b: torch.Tensor, slots: torch.Tensor,
+                             rank: int, scales: List[float]) -> None:
+    bank_delta_grouped(xs, ys, words, a_offs, b_offs, pool_a, pool_b, slots, rank, scales)
 
 
 @bank_lora_delta_grouped_.register_fake

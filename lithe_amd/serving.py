@@ -31,6 +31,7 @@ import torch
 from torch import nn
 
 from .kernels import _hip
+from .kernels import ops as _ops
 from .kernels.bank import PackedBank
 from .kernels.layers import IndexLoRALinear, PerSampleLoRALinear, replace_module, wrap_linears
 from .module import FLUX_TARGET_MODULES
@@ -38,6 +39,16 @@ from . import codebook as cb
 
 SHARED_INPUT_GROUPS = (("attn.to_q", "attn.to_k", "attn.to_v"),
                        ("attn.add_q_proj", "attn.add_k_proj", "attn.add_v_proj"))
+
+
+def _grouped_delta(xs, ys, words, a_offs, b_offs, pool_a, pool_b, slots, rank, scales) -> None:
+    """One grouped delta call: the torch.library op when traced (torch.compile), its body directly
+    in eager mode (no dispatcher on the host path)."""
+    if torch.compiler.is_compiling():
+        torch.ops.lithe_amd.bank_lora_delta_grouped_(xs, ys, words, a_offs, b_offs, pool_a, pool_b, slots, rank,
+                                                     scales)
+    else:
+        _ops.bank_delta_grouped(xs, ys, words, a_offs, b_offs, pool_a, pool_b, slots, rank, scales)
 
 
 def select_paths(paths: Sequence[str], module_set: str = "all") -> List[str]:
@@ -109,10 +120,9 @@ class SharedInputGroup:
                  else lead.assign.to(device=x.device, dtype=torch.int32).reshape(-1, 1).contiguous())
         # one grouped call: the members share one shrink job over x (one launch for the shrink,
         # one for every member's expand)
-        torch.ops.lithe_amd.bank_lora_delta_grouped_(
-            [x3] * len(self.layers), o3, lead._bank[0].words, [l._bank[1] for l in self.layers],
-            [l._bank[2] for l in self.layers], lead.pool_a, lead.pool_b, slots, lead.rank,
-            [l.scaling for l in self.layers])
+        _grouped_delta([x3] * len(self.layers), o3, lead._bank[0].words, [l._bank[1] for l in self.layers],
+                       [l._bank[2] for l in self.layers], lead.pool_a, lead.pool_b, slots, lead.rank,
+                       [l.scaling for l in self.layers])
         return [o.squeeze(1) if squeeze else o for o in o3]
 
     def _state(self, x: torch.Tensor):
@@ -206,9 +216,8 @@ class StageGroup:
         bsz = xs[0].shape[0]
         slots = (torch.zeros((bsz, 1), dtype=torch.int32, device=xs[0].device) if lead.assign is None
                  else lead.assign.to(device=xs[0].device, dtype=torch.int32).reshape(-1, 1).contiguous())
-        torch.ops.lithe_amd.bank_lora_delta_grouped_(
-            xs, ys, bank.words, [l._bank[1] for l in self.layers], [l._bank[2] for l in self.layers],
-            lead.pool_a, lead.pool_b, slots, lead.rank, [l.scaling for l in self.layers])
+        _grouped_delta(xs, ys, bank.words, [l._bank[1] for l in self.layers], [l._bank[2] for l in self.layers],
+                       lead.pool_a, lead.pool_b, slots, lead.rank, [l.scaling for l in self.layers])
         return outs
 
 
