@@ -25,6 +25,19 @@ int env_int(const char *name, int dflt) {
 
 int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
+// Shrink form of modules that read one input (n_mod modules of G1 rank groups each, `groups`
+// 16-token groups over the launch). Stacked: one workgroup per token tile carries every module's
+// rank groups, so x is staged once and each x fragment meets every module's A fragments.
+// Replicated: one single-module workgroup per (tile, module), x shared through L2. With two token
+// groups per wave the stacked form wins where its grid needs no K split (q / k / v sweep, one call
+// per module: 51.50 -> 50.43 ms; the 4,096-token calls 5.41 -> 5.70 TB/s) and loses on small grids
+// (512 tokens: 112 workgroups, 3.29 -> 2.72 TB/s). The caller checks n_mod * G1 <= kMaxGroups.
+// LITHE_SHARED_X_STACKED=1 / 0 forces either form.
+bool stack_shared(int64_t groups, int n_mod, int G1, int xbytes) {
+    if (const char *v = getenv("LITHE_SHARED_X_STACKED")) return atoi(v) != 0;
+    return xbytes == 2 && n_mod > 1 && n_mod * G1 <= kMaxGroups && groups >= 2048;
+}
+
 // Launch context of a grouped call: the plan rules that depend on the grid's size (the shrink's K
 // split, the expand's sub-tiles) see the whole grid of the launch, not one job.
 struct PlanCtx {
@@ -87,9 +100,12 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
         // thread; its registers matter more than the barriers of shorter pieces), up to 48 with
         // K split over 4 waves and more groups (fewer barriers), 16 with whole-K waves (the LDS of
         // a longer piece costs a workgroup of occupancy; measured over the FLUX shapes).
-        // Three groups: 8-block pieces keep the ring at 26 KB (4 workgroups per CU).
+        // Three groups: 8-block pieces keep the ring at 26 KB (4 workgroups per CU). Whole-K waves
+        // with two token groups each (half the workgroups) take 16-block pieces: the stacked
+        // q / k / v shrink at 4,096 tokens 5.69 -> 5.72 TB/s. (A K split keeps 8: its partition of K
+        // follows the piece size, and both token-group forms then give the same sums.)
         p.pb = std::max(1, std::min(ks >= 4 ? 48 : 16, fill_batch(p.GMs) * kThreads / (p.GMs * 16)));
-        if (p.GMs == 3) p.pb = std::min(8, fill_batch(3) * kThreads / (3 * 16));
+        if (p.GMs == 3 && (p.tw == 1 || ks > 1)) p.pb = std::min(8, fill_batch(3) * kThreads / (3 * 16));
         p.arow = p.pb * 16 + pad;
     }
     if (getenv("LITHE_SHRINK_PB")) {
@@ -417,11 +433,13 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
     if (!f || !y || !d_out || !out_scale) return LITHE_ERR_NULL;
     if (n_mod < 1 || n_mod > kMaxGroups) return LITHE_ERR_SHAPE;
     const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
-    // replicated form: a workgroup carries one module's rank groups; the stacked form carries all
-    const bool stacked = getenv("LITHE_SHARED_X_STACKED") != nullptr;
-    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, stacked ? n_mod : 1, workspace);
+    int32_t rc = check_call(x, x_dtype, n_batch, seq, d_in, y_dtype, rank, routes, n_rg, 1, workspace);
     if (rc || n_batch == 0 || seq == 0) return rc;
     const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
+    const int G1 = n_rg * routes->n_route;
+    // replicated form: a workgroup carries one module's rank groups; the stacked form carries all
+    const bool stacked = stack_shared(n_batch * ((seq + 15) / 16), n_mod, G1, xbytes);
+    if (stacked && n_mod * G1 > kMaxGroups) return LITHE_ERR_SHAPE;
     const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
     int64_t d_out_max = 1;
     for (int m = 0; m < n_mod; ++m) {
@@ -449,14 +467,12 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
     LoraArgs a{};
     a.a_src = make_src(f[0].a_idx);
     a.a_src.block_off = 0;
-    const int G1 = n_rg * routes->n_route;
     a.n_slots = f[0].a_idx.n_slots;
     copy_lut(a.luts.v[0], f[0].lut_a);
     set_call_fields(a, x, static_cast<int32_t *>(workspace), static_cast<char *>(workspace) + ps.off_mid, n_batch, seq,
                     d_in, rank, routes, mid_scale);
-    // Shrink: replicated (one single-module workgroup per tile and module, x shared through the
-    // Infinity Cache) unless LITHE_SHARED_X_STACKED asks for the module-stacked kernel (all
-    // modules' A rows as rank groups of one workgroup).
+    // Shrink: module-stacked (all modules' A rows as rank groups of one workgroup) or replicated
+    // (one single-module workgroup per tile and module, x shared through L2).
     Plan pshrink = ps;
     if (stacked) {
         for (int g = 0; g < kMaxGroups; ++g) a.a_goff[g] = f[std::min(g / G1, n_mod - 1)].a_idx.block_off;
@@ -604,10 +620,13 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
     a.G1 = G;
     const int src = src_of(a, LITHE_FACTOR_INDEXED);
 
-    // Modules that share an input run one workgroup per (tile, module) with x shared through L2
-    // (replicated). Stacking them as rank groups of one workgroup (3 groups for q / k / v) was
-    // measured at most 0.6 % faster on the fused FLUX sweep (16-block pieces; 8-block pieces 2 %
-    // slower): the stacked shrink holds 3 waves per SIMD.
+    // Modules that share an input: stacked (every job's modules as rank groups of one workgroup;
+    // one kernel serves the launch, so only when every job has the same module count) or
+    // replicated (one workgroup per tile and module, x shared through L2).
+    const int nm0 = L.n_in_sj[0];
+    bool stack = nm0 > 1 && nm0 * G <= kMaxGroups;
+    for (int q = 1; q < L.n_sj; ++q) stack = stack && L.n_in_sj[q] == nm0;
+    stack = stack && stack_shared(ctx.groups, nm0, G, xbytes);
     // shrink jobs, largest first (the short ones fill the tail of the grid)
     GroupArgs gs{};
     gs.a = a;
@@ -622,7 +641,8 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
         const int q = order[k];
         const lithe_module &md = mods[L.mods_of_sj[q][0]];
         const int nm = L.n_in_sj[q];
-        const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route, xbytes, false, ybytes, &ctx);
+        const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route * (stack ? nm : 1), xbytes,
+                                 false, ybytes, &ctx);
         ps[k] = p;
         set_shrink_fields(gs.a, p);       // G, n_rg (the same for every job)
         GroupJob &j = gs.job[k];
@@ -633,11 +653,12 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
         j.d_in = md.d_in;
         j.d_out = md.d_out;
         j.rows = n_batch * md.seq;
-        // the workgroups of module m (replicated) use a_goff[m]
-        for (int g = 0; g < kMaxGroups; ++g) j.a_goff[g] = mods[L.mods_of_sj[q][std::min(g, nm - 1)]].a_block_off;
+        // stacked: group g belongs to module g / G; replicated: the workgroups of module m use a_goff[m]
+        for (int g = 0; g < kMaxGroups; ++g)
+            j.a_goff[g] = mods[L.mods_of_sj[q][std::min(stack ? g / G : g, nm - 1)]].a_block_off;
         j.MR = nm * G * 16;
-        j.n_mod_wg = nm;
-        j.xnt = nm > 1 ? 0 : 1;
+        j.n_mod_wg = stack ? 1 : nm;
+        j.xnt = j.n_mod_wg > 1 ? 0 : 1;
         j.tiles_s = p.tiles_s;
         j.ks = p.ks;
         j.pb = p.pb;

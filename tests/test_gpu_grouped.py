@@ -9,6 +9,9 @@ one expand launch, modules given the same x sharing its shrink.
 * Without forcing, against the oracle within the bf16 tolerance of tests/test_gpu_delta.py.
 * The job-by-job form (LITHE_GROUPED_SERIAL: the per-call kernels, one launch per job) equals the
   grouped launch bit for bit.
+* Both shrink forms of modules that share an input (LITHE_SHARED_X_STACKED: the modules as rank
+  groups of one workgroup, or one workgroup per tile and module), forced, against the oracle and
+  the per-module calls.
 * Modules without tokens are skipped; a group at the real FLUX shapes (B = 14, 4,096 image and
   512 text tokens) equals the per-module calls bit for bit.
 * Rank 32 and 64 (2 and 4 rank groups), a three-entry mixture (three groups), the largest call
@@ -92,6 +95,7 @@ STAGE_FF = [("up", "a", 200), ("down", "b", 90), ("q", "c", 33)]
 def test_grouped_equals_per_module_calls(bank, monkeypatch, spec, ks, accumulate):
     _, bk, pools = bank
     monkeypatch.setenv("LITHE_SHRINK_KS", str(ks))
+    monkeypatch.setenv("LITHE_SHARED_X_STACKED", "0")
     g = torch.Generator(device="cuda").manual_seed(ks)
     xs, ys = _inputs(spec, g)
     slots = torch.tensor([3, 0, 4], dtype=torch.int32, device="cuda")
@@ -102,7 +106,10 @@ def test_grouped_equals_per_module_calls(bank, monkeypatch, spec, ks, accumulate
     assert workspace_errors() == 0
 
 
-def test_grouped_matches_oracle_and_serial_form(bank, monkeypatch):
+@pytest.mark.parametrize("form", [None, "1", "0"], ids=["auto", "stacked", "replicated"])
+def test_grouped_matches_oracle_and_serial_form(bank, monkeypatch, form):
+    if form is not None:
+        monkeypatch.setenv("LITHE_SHARED_X_STACKED", form)
     ads, bk, pools = bank
     g = torch.Generator(device="cuda").manual_seed(11)
     spec = STAGE_PROJ + [("up", "u", 64)]
@@ -119,6 +126,23 @@ def test_grouped_matches_oracle_and_serial_form(bank, monkeypatch):
     serial = _grouped(bk, pools, spec, xs, [y.clone() for y in ys], slots, accumulate=False)
     for (name, _, _), s, o in zip(spec, serial, got):
         assert torch.equal(s, o), name
+
+
+@pytest.mark.parametrize("accumulate", [True, False])
+def test_grouped_stacked_shared_inputs_equal_per_module_calls(bank, monkeypatch, accumulate):
+    """Stacked shared-input shrink with whole-K waves (two token groups per wave, the modules'
+    A rows as rank groups): each rank group's MFMA sequence is the per-module call's."""
+    _, bk, pools = bank
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    monkeypatch.setenv("LITHE_SHARED_X_STACKED", "1")
+    g = torch.Generator(device="cuda").manual_seed(21)
+    xs, ys = _inputs(STAGE_PROJ, g)
+    slots = torch.tensor([2, -1, 4], dtype=torch.int32, device="cuda")
+    want = _separate(bk, pools, STAGE_PROJ, xs, [y.clone() for y in ys], slots, accumulate)
+    got = _grouped(bk, pools, STAGE_PROJ, xs, [y.clone() for y in ys], slots, accumulate)
+    for (name, _, _), w, o in zip(STAGE_PROJ, want, got):
+        assert torch.equal(o, w), name
+    assert workspace_errors() == 0
 
 
 def test_grouped_mixture_routes(bank, monkeypatch):

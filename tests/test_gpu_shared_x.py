@@ -1,7 +1,9 @@
 """GPU parity of the shared-input call (lithe_lora_delta_shared_x): the q / k / v projections of
 one attention block read x once. Where both plans give every wave a whole K range the outputs
 equal three separate lithe_lora_delta calls bit for bit (same MFMA sequence per rank group);
-otherwise they match the oracle at the bf16 tolerance of the other delta tests."""
+otherwise they match the oracle at the bf16 tolerance of the other delta tests. Each test runs
+both shrink forms (LITHE_SHARED_X_STACKED: the modules as rank groups of one workgroup, or one
+workgroup per tile and module)."""
 import ctypes
 
 import numpy as np
@@ -46,7 +48,12 @@ def _run(bank, names, slots, seq, seed, rank=16):
     return x, y0, fused, sep
 
 
-def test_shared_x_equals_separate_calls_with_whole_k_waves():
+FORMS = pytest.mark.parametrize("form", ["1", "0"], ids=["stacked", "replicated"])
+
+
+@FORMS
+def test_shared_x_equals_separate_calls_with_whole_k_waves(monkeypatch, form):
+    monkeypatch.setenv("LITHE_SHARED_X_STACKED", form)
     _, bank = _bank()
     slots = torch.tensor([4, 1, 1, 0], dtype=torch.int32, device="cuda")
     _, y0, fused, sep = _run(bank, ["q", "k", "v"], slots, 8192, 1)      # 4 x 512 token groups: whole-K waves
@@ -56,7 +63,9 @@ def test_shared_x_equals_separate_calls_with_whole_k_waves():
 
 
 @pytest.mark.parametrize("names,seq", [(["q", "k", "v"], 77), (["q", "wide"], 130), (["k", "v", "q", "wide"], 33)])
-def test_shared_x_matches_oracle(names, seq):
+@FORMS
+def test_shared_x_matches_oracle(monkeypatch, form, names, seq):
+    monkeypatch.setenv("LITHE_SHARED_X_STACKED", form)
     ads, bank = _bank()
     slot_list = [3, -1, 0, 3]
     slots = torch.tensor(slot_list, dtype=torch.int32, device="cuda")
@@ -76,9 +85,11 @@ def test_shared_x_matches_oracle(names, seq):
         assert rel(got, to_np(ys)) < 2e-3, name
 
 
-def test_shared_x_mixture_routes_fill_all_groups():
+@FORMS
+def test_shared_x_mixture_routes_fill_all_groups(monkeypatch, form):
     """Two route entries x rank 16 x 3 modules = 6 rank groups (the 8-group kernels); one sample
     has a single entry (its second group is empty)."""
+    monkeypatch.setenv("LITHE_SHARED_X_STACKED", form)
     ads, bank = _bank()
     slot = torch.tensor([[0, 2], [4, -1], [1, 3]], dtype=torch.int32, device="cuda")
     w = torch.tensor([[0.7, 0.3], [1.0, 0.0], [0.5, 0.5]], device="cuda").sqrt().contiguous()
