@@ -209,10 +209,12 @@ class IndexLoRALinear(nn.Module):
         if not torch.compiler.is_compiling():
             # eager: the operator's body without the dispatcher, with the call descriptors kept
             # while the factors, tables and slot tensor stay the same (the kernels read the slot
-            # values at launch, so an in-place update of assign needs no new descriptor)
+            # values at launch, so an in-place update of assign needs no new descriptor). A bank's
+            # words are a view of its storage: a slot added within its capacity keeps the address
+            # and changes the slot count the descriptors carry.
             src = self._bank[0].words if self._bank is not None else self.idx_a
-            key = (x.dtype, src.data_ptr(), self.idx_b.data_ptr(), _hip.version_of(self.pool_a),
-                   _hip.version_of(self.pool_b), slots.data_ptr(), slots.shape[0])
+            key = (x.dtype, src.data_ptr(), src.shape[0], self.idx_b.data_ptr(), self.idx_b.shape[0],
+                   _hip.version_of(self.pool_a), _hip.version_of(self.pool_b), slots.data_ptr(), slots.shape[0])
             if self._eager is None or self._eager[0] != key:
                 self._eager = (key, self._factors(x.dtype), _delta.routes(slots))
             _, f, route = self._eager

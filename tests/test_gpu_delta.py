@@ -186,3 +186,32 @@ def test_bank_backed_index_layer():
     delta = odelta.shared_delta(to_np(x), _stack(ads, "l", "A"), opa, _stack(ads, "l", "B"), opb, [2, 1], 16, 384,
                                 1.0, "bf16")
     assert rel(got, odelta.index_linear(base_out, delta, "bf16")) < REL_BF16
+
+
+def test_bank_backed_layer_sees_slots_added_after_a_call():
+    """A slot added to the bank within its capacity (same storage, one more slot) after the layer
+    ran is routable by the next call: the layer's kept call descriptors follow the slot count."""
+    mods = [("l", 256, 384)]
+    ads = [random_adapter(mods, rank=16, seed=40 + s) for s in range(3)]
+    bank, words = PackedBank.from_adapters(ads, "cuda")       # capacity 3
+    bank.add(words[0])
+    bank.add(words[1])
+    base = torch.nn.Linear(256, 384).cuda().bfloat16()
+    layer = IndexLoRALinear.from_bank(base, bank, "l")
+    x = torch.randn(2, 40, 256, generator=torch.Generator().manual_seed(4)).bfloat16().cuda()
+    opa, opb = ocb.twin_pools()
+    ia, ib = _stack(ads, "l", "A"), _stack(ads, "l", "B")
+    lithe_amd.kernels.workspace_errors()                       # clears what earlier calls left
+    with torch.no_grad():
+        base_out = to_np(base(x))
+        layer.assign = torch.tensor([1, 0], device="cuda")
+        first = to_np(layer(x))
+        ptr = bank.words.data_ptr()
+        bank.add(words[2])
+        assert bank.words.data_ptr() == ptr and bank.num_slots == 3
+        layer.assign = torch.tensor([2, 1], device="cuda")
+        second = to_np(layer(x))
+    assert lithe_amd.kernels.workspace_errors() == 0
+    for got, assign in ((first, [1, 0]), (second, [2, 1])):
+        delta = odelta.shared_delta(to_np(x), ia, opa, ib, opb, assign, 16, 384, 1.0, "bf16")
+        assert rel(got, odelta.index_linear(base_out, delta, "bf16")) < REL_BF16, assign
