@@ -248,7 +248,9 @@ int32_t lithe_lora_delta_noalloc(const void *x, int32_t x_dtype, int64_t n_batch
  * that share one A index source (base, kind, levels, strides, n_slots; each module's A at its
  * own block_off) and one A value table; each module has its own B source and B table.
  * y, d_out, out_scale and factors are host arrays of n_mod entries (y[m] a device pointer).
- * n_mod * ceil(rank / 16) * n_route <= 8. Workspace: lithe_lora_workspace_bytes(n_batch, seq,
+ * ceil(rank / 16) * n_route <= 8. The shrink carries all modules in one workgroup per token tile
+ * when n_mod * ceil(rank / 16) * n_route <= 8 and the call is large (bf16 x, >= 2,048 16-token
+ * groups), else one workgroup per tile and module. Workspace: lithe_lora_workspace_bytes(n_batch, seq,
  * d_in, max d_out, rank, n_route * n_mod, x_dtype). LITHE_ERR_UNSUPPORTED if the A sources or
  * A tables differ, or a factor is DENSE.
  * Replaces three shared_codebook_lora_delta calls over one input (lithe/kernels/shared.py:197-263
