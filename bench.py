@@ -14,7 +14,7 @@ attention outputs, the two up and the two down projections, a single block's
 q / k / v) run as one grouped call: one shrink and one expand launch per stage,
 114 calls per sweep (``--config flux342``: one call per module).
 
-    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|ffn|hb|hb_modules|decode|ingest|encode] [--rank R]
+    python bench.py [--steps K] [--warmup W] [--config grouped|flux342|fused|qkv|decoded|decoded_grouped|ffn|hb|hb_modules|decode|ingest|encode] [--rank R]
 
 Prints ONE JSON line. ``value`` = tokens per second of the whole sweep;
 ``roofline`` covers the per-module delta call (shrink + expand kernels) against
@@ -97,8 +97,8 @@ class Workload:
 
         from lithe_amd.kernels import PackedBank, PackedLayout
         from lithe_amd.kernels.prepared import (group_workspace_bytes, prepare_dense, prepare_packed,
-                                                prepare_packed_group, prepare_packed_shared_x, shared_workspace,
-                                                shared_x_workspace_bytes, workspace_bytes)
+                                                prepare_packed_group, prepare_packed_shared_x, prepare_stacked_group,
+                                                shared_workspace, shared_x_workspace_bytes, workspace_bytes)
 
         self.name, self.mods, self.batch = name, mods, batch
         dev = torch.device("cuda:0")
@@ -158,10 +158,12 @@ class Workload:
             # per-module bf16 factors, then every module reads dense factors
             sel_of = {s: i for i, s in enumerate(uniq)}
             self.sel = torch.tensor([sel_of[int(s)] for s in assign], dtype=torch.int32, device=dev)
-            self.bank.decode_stacked(uniq)
+            self.stacked = torch.empty(len(uniq) * layout.total_blocks * layout.block_size, dtype=torch.bfloat16,
+                                       device=dev)
+            self.bank.decode_stacked(uniq, out=self.stacked)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            self.factors = self.bank.decode_stacked(uniq)
+            self.factors = self.bank.decode_stacked(uniq, out=self.stacked)
             torch.cuda.synchronize()
             self.decode_ms = (time.perf_counter() - t0) * 1e3
         for gi in groups:
@@ -177,8 +179,12 @@ class Workload:
                 xs.append(shared[key] if key is not None else x)
                 ys.append(buf(do, m, xs + ys))
                 offs.append(layout.module(n)[3:5])
-            self.calls.append(prepare_packed_group(xs, ys, self.bank.words, offs, 3, pools, self.assign, rank, 1.0,
-                                                   self.workspace, accumulate=True))
+            if decoded:    # module m's factors at its layout offsets of the stacked buffer
+                self.calls.append(prepare_stacked_group(xs, ys, self.stacked, len(uniq), offs, self.sel, rank, 1.0,
+                                                        self.workspace, accumulate=True))
+            else:
+                self.calls.append(prepare_packed_group(xs, ys, self.bank.words, offs, 3, pools, self.assign, rank,
+                                                       1.0, self.workspace, accumulate=True))
             self.call_mods.append([mods[i] for i in gi])
         k = len(mods) if grouped else 0
         while k < len(mods):
@@ -692,7 +698,8 @@ def main():
                     "whose step is 0.35 ms)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 3; 20 for --config ffn)")
     ap.add_argument("--config", default="grouped",
-                    choices=["grouped", "flux342", "fused", "qkv", "decoded", "ffn", "hb", "hb_modules", "decode",
+                    choices=["grouped", "flux342", "fused", "qkv", "decoded", "decoded_grouped", "ffn", "hb",
+                             "hb_modules", "decode",
                              "ingest", "encode"])
     ap.add_argument("--rank", type=int, default=RANK, help="adapter rank (a multiple of 16; the headline and the "
                     "decode's first line are rank 16, its second rank 64)")
@@ -726,19 +733,19 @@ def main():
         run_encode(args)
         return
     rng = np.random.default_rng(1234)
-    if args.config in ("flux342", "decoded", "qkv", "grouped", "fused"):
+    if args.config in ("flux342", "decoded", "decoded_grouped", "qkv", "grouped", "fused"):
         mods, batch, n_slots = flux_modules(4096, 512), 14, args.slots or 10_000
         assign = rng.choice(n_slots, batch, replace=False)
-        wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config == "decoded",
-                      qkv=args.config in ("qkv", "fused"), grouped=args.config in ("grouped", "fused"),
-                      rank=args.rank)
+        wl = Workload(args.config, mods, batch, n_slots, assign, decoded=args.config in ("decoded", "decoded_grouped"),
+                      qkv=args.config in ("qkv", "fused"),
+                      grouped=args.config in ("grouped", "fused", "decoded_grouped"), rank=args.rank)
         workload = "FLUX.1-dev 342 linears, 1024^2: B=14 x 4608 tokens (4096 img + 512 txt), 10k-adapter packed bank"
-        if args.config == "decoded":
+        if args.config in ("decoded", "decoded_grouped"):
             workload += (", decoded mode: the 14 routed adapters decoded once to stacked bf16 factors "
                          "(decode-on-swap), modules read dense factors")
         if args.config in ("qkv", "fused"):
             workload += ", q/k/v fused: the three projections of each attention input read x once"
-        if args.config in ("grouped", "fused"):
+        if args.config in ("grouped", "fused", "decoded_grouped"):
             workload += (", grouped: the independent linears of each block stage (image + text projections, "
                          "attention outputs, up and down projections) in one shrink + one expand launch")
         if args.config != "flux342":
@@ -784,7 +791,7 @@ def main():
         _, di, do, m = group[0]
         if len(group) == 1:
             k = f"{di}->{do} x {m}"
-        elif args.config in ("grouped", "fused", "hb"):
+        elif args.config in ("grouped", "fused", "hb", "decoded_grouped"):
             k = "group " + " + ".join(sorted({f"{g[1]}->{g[2]} x {g[3]}" for g in group}))
         else:
             k = f"{di}->{len(group)}x{do} x {m} (shared x)"
@@ -826,7 +833,9 @@ def main():
                                 "grouped": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)",
                                 "fused": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage, "
                                          "q/k/v sharing x)",
-                                "hb": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)"}.get(
+                                "hb": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)",
+                                "decoded_grouped": "lithe_lora_delta_grouped over dense stacked factors (one shrink + "
+                                                   "one expand launch per block stage)"}.get(
                                     args.config,
                                                                  "lithe_lora_delta (shrink + expand, one call per module)"),
                      "bound": "hbm",

@@ -285,7 +285,10 @@ int64_t lithe_lora_grouped_workspace_bytes(int64_t n_batch, int32_t n_mod, const
  * the same x, seq and d_in share one shrink over x (x read once, as lithe_lora_delta_shared_x).
  * Every module uses the same routes, rank and dtypes, and the same index sources and value tables
  * (factors: one INDEXED entry whose a_idx / b_idx block_off are ignored: each module's offsets come
- * from a_block_off / b_block_off). The launch plan is made for the whole grid, so the K split of a
+ * from a_block_off / b_block_off). Decoded mode: one DENSE entry over stacked factors in the layout
+ * lithe_decode_stacked writes (module m's A (n_dense, rank, d_in) at element n_dense * 64 *
+ * a_block_off of dense_a, its B (n_dense, d_out, rank) at n_dense * 64 * b_block_off of dense_b; the
+ * caller keeps them inside its buffers; no weight_sqrt / slot_scale). The launch plan is made for the whole grid, so the K split of a
  * module's shrink can differ from its lithe_lora_delta plan (the fp32 sums are then grouped
  * differently). Modules with seq == 0 are skipped. Outputs of two modules must not overlap
  * (LITHE_ERR_OVERLAP); an output may alias another module's input (every shrink ends before the

@@ -192,7 +192,7 @@ Plan make_plan(int64_t n_batch, int64_t seq, int64_t d_in, int64_t d_out, int ra
 
 // The grouped kernels are compiled for bf16 activations and outputs with packed 3-level factors.
 bool launch_shrink_group_bf16_ok(int x_dtype, int y_dtype, int src) {
-    return x_dtype == LITHE_DT_BF16 && y_dtype == LITHE_DT_BF16 && src == SRC_PACKED;
+    return x_dtype == LITHE_DT_BF16 && y_dtype == LITHE_DT_BF16 && (src == SRC_PACKED || src == SRC_DENSE);
 }
 
 int src_of(const LoraArgs &a, int kind) {
@@ -566,7 +566,8 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
                                             int64_t workspace_bytes, void *stream) {
     if (!mods_in || !f) return LITHE_ERR_NULL;
     if (n_mod < 1 || n_mod > kMaxJobs) return LITHE_ERR_SHAPE;
-    if (f->kind != LITHE_FACTOR_INDEXED) return LITHE_ERR_UNSUPPORTED;
+    const bool dense = f->kind == LITHE_FACTOR_DENSE;
+    if (f->kind != LITHE_FACTOR_INDEXED && !dense) return LITHE_ERR_UNSUPPORTED;
     const int n_rg = rank > 0 ? (rank + 15) / 16 : 1;
     const int xbytes = x_dtype == LITHE_DT_BF16 ? 2 : 4;
     const int ybytes = y_dtype == LITHE_DT_BF16 ? 2 : 4;
@@ -582,11 +583,15 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
         if ((md.d_out * rank) % kBlock) return LITHE_ERR_ALIGN;
         if (!md.y) return LITHE_ERR_NULL;
         if ((uintptr_t)md.y & (uintptr_t)(ybytes - 1)) return LITHE_ERR_ALIGN;
-        lithe_factors fm = *f;
-        fm.a_idx.block_off = md.a_block_off;
-        fm.b_idx.block_off = md.b_block_off;
-        rc = check_indexed(&fm, rank, md.d_in, md.d_out);
-        if (rc) return rc;
+        if (dense) {
+            if (md.a_block_off < 0 || md.b_block_off < 0) return LITHE_ERR_SHAPE;
+        } else {
+            lithe_factors fm = *f;
+            fm.a_idx.block_off = md.a_block_off;
+            fm.b_idx.block_off = md.b_block_off;
+            rc = check_indexed(&fm, rank, md.d_in, md.d_out);
+            if (rc) return rc;
+        }
         mods[n_act++] = md;
     }
     if (n_act == 0) return LITHE_OK;
@@ -608,23 +613,36 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
     // common fields; each job's fields are applied over them
     char *ws = static_cast<char *>(workspace);
     LoraArgs a{};
-    a.a_src = make_src(f->a_idx);
-    a.a_src.block_off = 0;
-    a.b_src = make_src(f->b_idx);
-    a.n_slots = std::min(f->a_idx.n_slots, f->b_idx.n_slots);
-    copy_lut(a.luts.v[0], f->lut_a);
-    copy_lut(a.luts.v[1], f->lut_b);
+    if (dense) {
+        // module m's A / B: the (n_dense, rank, d_in) / (n_dense, d_out, rank) stacks at elements
+        // n_dense * 64 * a_block_off / b_block_off of dense_a / dense_b (lithe_decode_stacked's layout)
+        if (!f->dense_a || !f->dense_b) return LITHE_ERR_NULL;
+        if (f->dense_dtype != x_dtype) return LITHE_ERR_DTYPE;
+        if (f->n_dense < 1) return LITHE_ERR_SHAPE;
+        if (((uintptr_t)f->dense_a & 15u) || ((uintptr_t)f->dense_b & 15u)) return LITHE_ERR_ALIGN;
+        if (routes->weight_sqrt || routes->slot_scale) return LITHE_ERR_UNSUPPORTED;
+        a.dense_a = f->dense_a;
+        a.dense_b = f->dense_b;
+        a.n_slots = f->n_dense;
+    } else {
+        a.a_src = make_src(f->a_idx);
+        a.a_src.block_off = 0;
+        a.b_src = make_src(f->b_idx);
+        a.n_slots = std::min(f->a_idx.n_slots, f->b_idx.n_slots);
+        copy_lut(a.luts.v[0], f->lut_a);
+        copy_lut(a.luts.v[1], f->lut_b);
+    }
     set_call_fields(a, mods[0].x, reinterpret_cast<int32_t *>(ws), ws + L.mid_off[0], n_batch, mods[0].seq,
                     mods[0].d_in, rank, routes, nullptr);
     set_module_fields(a, mods[0].y, mods[0].d_out, accumulate, 1.0f, nullptr);
     a.G1 = G;
-    const int src = src_of(a, LITHE_FACTOR_INDEXED);
+    const int src = src_of(a, f->kind);
 
     // Modules that share an input: stacked (every job's modules as rank groups of one workgroup;
     // one kernel serves the launch, so only when every job has the same module count) or
     // replicated (one workgroup per tile and module, x shared through L2).
     const int nm0 = L.n_in_sj[0];
-    bool stack = nm0 > 1 && nm0 * G <= kMaxGroups;
+    bool stack = !dense && nm0 > 1 && nm0 * G <= kMaxGroups;
     for (int q = 1; q < L.n_sj; ++q) stack = stack && L.n_in_sj[q] == nm0;
     stack = stack && stack_shared(ctx.groups, nm0, G, xbytes);
     // shrink jobs, largest first (the short ones fill the tail of the grid)
@@ -642,7 +660,7 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
         const lithe_module &md = mods[L.mods_of_sj[q][0]];
         const int nm = L.n_in_sj[q];
         const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route * (stack ? nm : 1), xbytes,
-                                 false, ybytes, &ctx);
+                                 dense, ybytes, &ctx);
         ps[k] = p;
         set_shrink_fields(gs.a, p);       // G, n_rg (the same for every job)
         GroupJob &j = gs.job[k];
@@ -686,7 +704,7 @@ extern "C" int32_t lithe_lora_delta_grouped(int32_t n_mod, const lithe_module *m
     for (int k = 0; k < n_act; ++k) {
         const int m = order[k];
         const lithe_module &md = mods[m];
-        const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route, xbytes, false, ybytes, &ctx);
+        const Plan p = make_plan(n_batch, md.seq, md.d_in, md.d_out, rank, routes->n_route, xbytes, dense, ybytes, &ctx);
         pe[k] = p;
         set_shrink_fields(ge.a, p);
         GroupJob &j = ge.job[k];

@@ -429,8 +429,12 @@ __device__ __forceinline__ void shrink_body(const LoraArgs &a, int bid, const in
                 const int gr = it / per_row, c = it - gr * per_row;
                 const int grp = gr >> 4, rr = (grp % a.n_rg) * 16 + (gr & 15);
                 const bool live = group_slot(grp) >= 0 && rr < a.rank;
-                const int64_t off =
-                    live ? ((int64_t)group_slot(grp) * a.rank + rr) * a.d_in + (int64_t)g * pb * kBlock + c * EV : 0;
+                // group_aoff: the module's A in a stacked buffer of several modules' factors
+                // (grouped calls), n_slots (= n_dense) selections per factor; 0 for one module
+                const int64_t off = live ? group_aoff(grp) * kBlock * a.n_slots +
+                                               ((int64_t)group_slot(grp) * a.rank + rr) * a.d_in +
+                                               (int64_t)g * pb * kBlock + c * EV
+                                         : 0;
                 v[q] = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_a) + off);
             }
 #pragma unroll
@@ -935,8 +939,10 @@ __device__ __forceinline__ void expand_body(const LoraArgs &a, int bid) {
             float w, sc;
             route_pick(j, slot, w, sc);
             f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            // b_src.block_off: the module's B in a stacked buffer (grouped calls), else 0
             if (slot >= 0)
                 v = *reinterpret_cast<const f32x4 *>(static_cast<const XT *>(a.dense_b) +
+                                                     a.b_src.block_off * kBlock * a.n_slots +
                                                      (slot * a.d_out + obase_wg) * a.rank + (int64_t)c * EV);
             *reinterpret_cast<f32x4 *>(bp + (int64_t)j * BOW * a.rank + (int64_t)c * EV) = v;
         }
@@ -1386,46 +1392,64 @@ void launch_expand_group(const GroupArgs &g, unsigned grid, size_t lds, hipStrea
 // TW: token groups per wave (2 only with several rank groups).
 template <typename XT, int SRC>
 void dispatch_shrink_group(int GM, int TW, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
-    if (TW == 2) {
+    if constexpr (SRC == SRC_DENSE) {    // dense factors: one token group per wave, no 3-group kernel
         switch (GM) {
-            case 2: launch_shrink_group<XT, SRC, 2, 2>(g, grid, lds, st); break;
-            case 3: launch_shrink_group<XT, SRC, 3, 2>(g, grid, lds, st); break;
-            case 4: launch_shrink_group<XT, SRC, 4, 2>(g, grid, lds, st); break;
-            default: launch_shrink_group<XT, SRC, 8, 2>(g, grid, lds, st); break;
+            case 1: launch_shrink_group<XT, SRC, 1>(g, grid, lds, st); break;
+            case 2: launch_shrink_group<XT, SRC, 2>(g, grid, lds, st); break;
+            case 4: launch_shrink_group<XT, SRC, 4>(g, grid, lds, st); break;
+            default: launch_shrink_group<XT, SRC, 8>(g, grid, lds, st); break;
         }
-        return;
-    }
-    switch (GM) {
-        case 1: launch_shrink_group<XT, SRC, 1>(g, grid, lds, st); break;
-        case 2: launch_shrink_group<XT, SRC, 2>(g, grid, lds, st); break;
-        case 3: launch_shrink_group<XT, SRC, 3>(g, grid, lds, st); break;
-        case 4: launch_shrink_group<XT, SRC, 4>(g, grid, lds, st); break;
-        default: launch_shrink_group<XT, SRC, 8>(g, grid, lds, st); break;
+    } else {
+        if (TW == 2) {
+            switch (GM) {
+                case 2: launch_shrink_group<XT, SRC, 2, 2>(g, grid, lds, st); break;
+                case 3: launch_shrink_group<XT, SRC, 3, 2>(g, grid, lds, st); break;
+                case 4: launch_shrink_group<XT, SRC, 4, 2>(g, grid, lds, st); break;
+                default: launch_shrink_group<XT, SRC, 8, 2>(g, grid, lds, st); break;
+            }
+            return;
+        }
+        switch (GM) {
+            case 1: launch_shrink_group<XT, SRC, 1>(g, grid, lds, st); break;
+            case 2: launch_shrink_group<XT, SRC, 2>(g, grid, lds, st); break;
+            case 3: launch_shrink_group<XT, SRC, 3>(g, grid, lds, st); break;
+            case 4: launch_shrink_group<XT, SRC, 4>(g, grid, lds, st); break;
+            default: launch_shrink_group<XT, SRC, 8>(g, grid, lds, st); break;
+        }
     }
 }
 
 // BOM as in dispatch_expand (bf16 activations); GM counts effective groups of NS rank groups.
 template <typename XT, typename YT, int SRC>
 void dispatch_expand_group(int GM, int BOM, int NS, const GroupArgs &g, unsigned grid, size_t lds, hipStream_t st) {
-    if (NS == 4) {
-        if (GM == 1) launch_expand_group<XT, YT, SRC, 1, 256, 4>(g, grid, lds, st);
-        else launch_expand_group<XT, YT, SRC, 2, 256, 4>(g, grid, lds, st);
-        return;
-    }
-    if (NS == 2) {
-        if (GM == 1) launch_expand_group<XT, YT, SRC, 1, 256, 2>(g, grid, lds, st);
-        else if (GM == 2) launch_expand_group<XT, YT, SRC, 2, 256, 2>(g, grid, lds, st);
-        else launch_expand_group<XT, YT, SRC, 4, 128, 2>(g, grid, lds, st);
-        return;
-    }
-    switch (GM) {
-        case 1:
-            if (BOM == 256) launch_expand_group<XT, YT, SRC, 1, 256>(g, grid, lds, st);
-            else launch_expand_group<XT, YT, SRC, 1, 128>(g, grid, lds, st);
-            break;
-        case 2: launch_expand_group<XT, YT, SRC, 2, 256>(g, grid, lds, st); break;
-        case 4: launch_expand_group<XT, YT, SRC, 4, 128>(g, grid, lds, st); break;
-        default: launch_expand_group<XT, YT, SRC, 8, 64>(g, grid, lds, st); break;
+    if constexpr (SRC == SRC_DENSE) {    // dense factors: no rank collapse, 256 outputs per wave at one group
+        switch (GM) {
+            case 1: launch_expand_group<XT, YT, SRC, 1, 256>(g, grid, lds, st); break;
+            case 2: launch_expand_group<XT, YT, SRC, 2, 256>(g, grid, lds, st); break;
+            case 4: launch_expand_group<XT, YT, SRC, 4, 128>(g, grid, lds, st); break;
+            default: launch_expand_group<XT, YT, SRC, 8, 64>(g, grid, lds, st); break;
+        }
+    } else {
+        if (NS == 4) {
+            if (GM == 1) launch_expand_group<XT, YT, SRC, 1, 256, 4>(g, grid, lds, st);
+            else launch_expand_group<XT, YT, SRC, 2, 256, 4>(g, grid, lds, st);
+            return;
+        }
+        if (NS == 2) {
+            if (GM == 1) launch_expand_group<XT, YT, SRC, 1, 256, 2>(g, grid, lds, st);
+            else if (GM == 2) launch_expand_group<XT, YT, SRC, 2, 256, 2>(g, grid, lds, st);
+            else launch_expand_group<XT, YT, SRC, 4, 128, 2>(g, grid, lds, st);
+            return;
+        }
+        switch (GM) {
+            case 1:
+                if (BOM == 256) launch_expand_group<XT, YT, SRC, 1, 256>(g, grid, lds, st);
+                else launch_expand_group<XT, YT, SRC, 1, 128>(g, grid, lds, st);
+                break;
+            case 2: launch_expand_group<XT, YT, SRC, 2, 256>(g, grid, lds, st); break;
+            case 4: launch_expand_group<XT, YT, SRC, 4, 128>(g, grid, lds, st); break;
+            default: launch_expand_group<XT, YT, SRC, 8, 64>(g, grid, lds, st); break;
+        }
     }
 }
 

@@ -240,3 +240,29 @@ def prepare_packed_group(xs: Sequence[torch.Tensor], ys: Sequence[torch.Tensor],
     sl = slots.to(device=xs[0].device, dtype=torch.int32).reshape(-1, 1).contiguous()
     return PreparedGroup(xs, ys, f, offsets, _delta.routes(sl), rank, [scaling] * len(xs), workspace, accumulate,
                          keep=(sl, bank_words))
+
+
+def prepare_stacked_group(xs: Sequence[torch.Tensor], ys: Sequence[torch.Tensor], stacked: torch.Tensor, n_sel: int,
+                          offsets: Sequence[Tuple[int, int]], slots: torch.Tensor, rank: int, scaling: float,
+                          workspace: torch.Tensor, accumulate: bool = True) -> PreparedGroup:
+    """Prepared grouped decoded-mode deltas: ``stacked`` is a ``decode_packed_stacked`` buffer of
+    ``n_sel`` selections (module m's A / B at elements n_sel * 64 * a_off / b_off of it, offsets
+    [(a_off, b_off)] of the bank layout); sample i uses selection ``slots[i]``. Each module gets
+    what ``prepare_dense`` over its views of the buffer computes."""
+    _hip.require_gpu(stacked)
+    if stacked.dim() != 1 or not stacked.is_contiguous() or stacked.dtype != xs[0].dtype:
+        raise ValueError("stacked factors must be a flat contiguous buffer in the activation dtype")
+    if n_sel < 1:
+        raise ValueError("n_sel must be >= 1")
+    for (ao, bo), x, y in zip(offsets, xs, ys):
+        end = max(n_sel * 64 * int(ao) + n_sel * rank * x.shape[2], n_sel * 64 * int(bo) + n_sel * y.shape[2] * rank)
+        if int(ao) < 0 or int(bo) < 0 or end > stacked.numel():
+            raise ValueError(f"offsets ({ao}, {bo}) reach past the stacked buffer of {stacked.numel()} elements")
+    f = _hip.Factors()
+    f.kind = _hip.FACTOR_DENSE
+    f.dense_dtype = _hip.dtype_code(stacked.dtype)
+    f.dense_a = f.dense_b = stacked.data_ptr()
+    f.n_dense = int(n_sel)
+    sl = slots.to(device=xs[0].device, dtype=torch.int32).reshape(-1, 1).contiguous()
+    return PreparedGroup(xs, ys, f, offsets, _delta.routes(sl), rank, [scaling] * len(xs), workspace, accumulate,
+                         keep=(sl, stacked))

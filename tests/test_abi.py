@@ -322,8 +322,9 @@ def test_noalloc_delta_argument_errors_before_any_launch():
 
 
 def test_grouped_argument_errors_and_workspace_bytes():
-    """lithe_lora_delta_grouped: per-module checks of lithe_lora_delta, the module limit, indexed
-    factors only, the workspace of one intermediate per distinct input; no call reaches a launch."""
+    """lithe_lora_delta_grouped: per-module checks of lithe_lora_delta, the module limit, the checks
+    of dense (stacked) factors, the workspace of one intermediate per distinct input; no call
+    reaches a launch."""
     lib = _hip.load()
     f, words = _indexed(n_slots=4, d_in=128, d_out=64)
     slot = np.zeros(2, dtype=np.int32)
@@ -339,18 +340,33 @@ def test_grouped_argument_errors_and_workspace_bytes():
             arr[i].a_block_off, arr[i].b_block_off, arr[i].out_scale = 0, 32, 1.0
         return arr
 
-    def call(arr, n, fa=f, wsb=1 << 20, n_batch=2, ws=1 << 12):
+    def call(arr, n, fa=f, wsb=1 << 20, n_batch=2, ws=1 << 12, rt=route):
         return lib.lithe_lora_delta_grouped(n, arr, _hip.DT_BF16, _hip.DT_BF16, n_batch, 1, 16,
-                                            ctypes.byref(fa) if fa else None, ctypes.byref(route),
+                                            ctypes.byref(fa) if fa else None, ctypes.byref(rt),
                                             ctypes.c_void_p(ws), wsb, None)
 
     assert call(None, 2) == _hip.ERR_NULL
     assert call(mods(2), 2, fa=None) == _hip.ERR_NULL
     assert call(mods(1), 0) == _hip.ERR_SHAPE
     assert call(mods(9), 9) == _hip.ERR_SHAPE                                 # more than 8 modules
-    dense = _hip.Factors()
-    dense.kind = _hip.FACTOR_DENSE
-    assert call(mods(2), 2, fa=dense) == _hip.ERR_UNSUPPORTED
+    dense = _hip.Factors()                                                    # stacked dense factors
+    dense.kind, dense.dense_dtype, dense.n_dense = _hip.FACTOR_DENSE, _hip.DT_BF16, 4
+    assert call(mods(2, distinct=True), 2, fa=dense) == _hip.ERR_NULL         # no factor buffers
+    dense.dense_a = dense.dense_b = 1 << 14
+    dense.dense_dtype = _hip.DT_F32
+    assert call(mods(2, distinct=True), 2, fa=dense) == _hip.ERR_DTYPE        # not the activation dtype
+    dense.dense_dtype, dense.n_dense = _hip.DT_BF16, 0
+    assert call(mods(2, distinct=True), 2, fa=dense) == _hip.ERR_SHAPE
+    dense.n_dense, dense.dense_a = 4, (1 << 14) + 8
+    assert call(mods(2, distinct=True), 2, fa=dense) == _hip.ERR_ALIGN
+    dense.dense_a = 1 << 14
+    w = np.ones(2, dtype=np.float32)
+    weighted = _hip.Routes(slot=slot.ctypes.data, weight_sqrt=w.ctypes.data, slot_scale=None, n_route=1)
+    assert call(mods(2, distinct=True), 2, fa=dense, rt=weighted) == _hip.ERR_UNSUPPORTED
+    neg = mods(2, distinct=True)
+    neg[1].a_block_off = -1
+    assert call(neg, 2, fa=dense) == _hip.ERR_SHAPE
+    assert call(mods(2), 2, fa=dense) == _hip.ERR_OVERLAP
     assert call(mods(2, x=(1 << 12) + 8), 2) == _hip.ERR_ALIGN               # x not 16-byte aligned
     assert call(mods(2, d_out=6), 2) == _hip.ERR_ALIGN                       # d_out * rank % 64
     assert call(mods(2, y=0), 2) == _hip.ERR_NULL

@@ -150,3 +150,63 @@ def test_decode_stacked_from_int16_source_matches_packed():
     torch.cuda.synchronize()
     for name in lay.names:
         assert torch.equal(got[name][0], want[name][0]) and torch.equal(got[name][1], want[name][1])
+
+
+@pytest.mark.parametrize("accumulate", [True, False])
+def test_grouped_decoded_mode_equals_per_module_dense_calls(monkeypatch, accumulate):
+    """lithe_lora_delta_grouped over dense factors in the stacked decode layout (one buffer; module
+    m's A / B at n_sel * 64 * a_off / b_off): with the shrink's K split fixed, every module's output
+    equals the per-module decoded-mode call over its views of the buffer bit for bit. Covers
+    modules sharing one x (one workgroup per tile and module), different widths, a 12,288-wide
+    input and an empty route."""
+    from lithe_amd.kernels import decode_packed_stacked
+    from lithe_amd.kernels.prepared import prepare_stacked_group
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    mods = [("q", 512, 512), ("k", 512, 512), ("v", 512, 512), ("up", 512, 2048), ("down", 2048, 512)]
+    _, bank = _bank(mods, 4, 90)
+    uniq = [3, 0, 2]
+    u = torch.tensor(uniq, dtype=torch.int32, device="cuda")
+    buf = decode_packed_stacked(bank.words, u, bank.layout, bank.pool_a, bank.pool_b)
+    st = bank.decode_stacked(uniq)
+    sel = torch.tensor([2, -1, 0, 1], dtype=torch.int32, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(17)
+    shape = {n: (di, do) for n, di, do in mods}
+    spec = [("q", 96), ("k", 96), ("v", 96), ("up", 40), ("down", 33)]
+    xq = torch.randn(4, 96, 512, device="cuda", generator=gen).bfloat16()
+    xs = [xq if n in ("q", "k", "v") else torch.randn(4, m, shape[n][0], device="cuda", generator=gen).bfloat16()
+          for n, m in spec]
+    y0 = [torch.randn(4, m, shape[n][1], device="cuda", generator=gen).bfloat16() for n, m in spec]
+    ws = shared_workspace("cuda", 16 << 20)
+    offs = [bank.layout.module(n)[3:5] for n, _ in spec]
+    got = [y.clone() for y in y0]
+    prepare_stacked_group(xs, got, buf, len(uniq), offs, sel, 16, 0.75, ws, accumulate)()
+    want = [y.clone() for y in y0]
+    for (n, _), x, y in zip(spec, xs, want):
+        prepare_dense(x, y, st[n][0], st[n][1], sel, 16, 0.75, ws, accumulate)()
+    torch.cuda.synchronize()
+    for (n, _), g, w, y in zip(spec, got, want, y0):
+        assert torch.equal(g, w), n
+        assert not torch.equal(g[0], y[0]), n
+    assert _hip.workspace_errors() == 0
+
+
+def test_grouped_decoded_mode_rejects_weighted_routes():
+    from lithe_amd.kernels import decode_packed_stacked
+    from lithe_amd.kernels.prepared import PreparedGroup
+    _, bank = _bank(SMALL, 2, 95)
+    u = torch.tensor([1, 0], dtype=torch.int32, device="cuda")
+    buf = decode_packed_stacked(bank.words, u, bank.layout, bank.pool_a, bank.pool_b)
+    name, d_in, d_out = SMALL[0]
+    x = torch.zeros(2, 16, d_in, dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros(2, 16, d_out, dtype=torch.bfloat16, device="cuda")
+    f = _hip.Factors()
+    f.kind = _hip.FACTOR_DENSE
+    f.dense_dtype = _hip.dtype_code(buf.dtype)
+    f.dense_a = f.dense_b = buf.data_ptr()
+    f.n_dense = 2
+    slots = torch.tensor([[0], [1]], dtype=torch.int32, device="cuda")
+    w = torch.ones(2, 1, device="cuda")
+    call = PreparedGroup([x], [y], f, [bank.layout.module(name)[3:5]], _delta.routes(slots, w), 16, [1.0],
+                         shared_workspace("cuda", 1 << 20), keep=(slots, w, buf))
+    with pytest.raises(ValueError):
+        call()
