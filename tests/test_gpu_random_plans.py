@@ -3,7 +3,7 @@ rank groups; the rank collapse at 32, 64, 96 and 128), per-call and grouped laun
 modules with their own token counts or all reading one x (the shared-input shrink), bf16 and fp32
 outputs, write and accumulate mode, and random
 plan overrides (waves along the outputs, expand sub-tiles, the shrink's K split and token groups
-per wave, the rank collapse off). Every plan computes the same delta up to the fp32 summation
+per wave, the rank collapse off, the shared-input shrink form). Every plan computes the same delta up to the fp32 summation
 order, so each case must meet the bf16 tolerance of tests/test_gpu_delta.py (rel-Frobenius 2e-3
 against the oracle; 1e-2 on the change of an accumulated bf16 output, which includes the rounding
 of y + delta). A second sweep runs serve.py's mixture routing."""
@@ -26,7 +26,8 @@ from helpers import random_adapter, rel
 pytestmark = pytest.mark.gpu
 
 KNOBS = {"LITHE_EXPAND_WO": ["1", "2", "4"], "LITHE_EXPAND_SUBS": ["1", "2", "4", "8"],
-         "LITHE_SHRINK_KS": ["1", "2", "4"], "LITHE_SHRINK_TW": ["1", "2"], "LITHE_EXPAND_NS": ["1"]}
+         "LITHE_SHRINK_KS": ["1", "2", "4"], "LITHE_SHRINK_TW": ["1", "2"], "LITHE_EXPAND_NS": ["1"],
+         "LITHE_SHARED_X_STACKED": ["0", "1"]}
 
 
 def _case(rng, monkeypatch):
