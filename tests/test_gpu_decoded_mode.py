@@ -210,3 +210,53 @@ def test_grouped_decoded_mode_rejects_weighted_routes():
                          shared_workspace("cuda", 1 << 20), keep=(slots, w, buf))
     with pytest.raises(ValueError):
         call()
+
+
+def test_random_grouped_decoded_mode_equals_per_module(monkeypatch):
+    """Seeded random grouped decoded-mode calls: ranks 16-128 (one to eight rank groups), one to
+    four modules with their own inputs and token counts or one shared x, 12,288-wide inputs, empty
+    routes, write and accumulate mode, against per-module dense calls over views of the same
+    stacked buffer with the K split fixed: bit for bit."""
+    from lithe_amd.kernels import decode_packed_stacked, split_stacked
+    from lithe_amd.kernels.prepared import prepare_stacked_group
+    monkeypatch.setenv("LITHE_SHRINK_KS", "1")
+    rng = np.random.default_rng(5)
+    ws = shared_workspace("cuda", 64 << 20)
+    for n in range(24):
+        rank = int(rng.choice([16, 32, 48, 64, 128]))
+        n_mod = int(rng.integers(1, 5))
+        share = n_mod > 1 and bool(rng.integers(0, 2))
+        d_in0 = 12288 if rng.integers(0, 5) == 0 else int(rng.integers(1, 17)) * 64
+        mods = [(f"m{m}", d_in0 if share or m == 0 else int(rng.integers(1, 17)) * 64, int(rng.integers(2, 300)) * 4)
+                for m in range(n_mod)]
+        batch = int(rng.integers(1, 5))
+        seq0 = int(rng.integers(1, 200))
+        seqs = [seq0 if share else int(rng.integers(1, 200)) for _ in range(n_mod)]
+        n_ad = int(rng.integers(1, 5))
+        ads = [random_adapter([(nm, di, do) for nm, di, do in mods], rank=rank, seed=int(rng.integers(0, 1 << 30)))
+               for _ in range(n_ad)]
+        bank, words = PackedBank.from_adapters(ads, "cuda")
+        for w in words:
+            bank.add(w)
+        uniq = sorted(set(rng.integers(0, n_ad, int(rng.integers(1, n_ad + 1))).tolist()))
+        u = torch.tensor(uniq, dtype=torch.int32, device="cuda")
+        buf = decode_packed_stacked(bank.words, u, bank.layout, bank.pool_a, bank.pool_b)
+        st = split_stacked(buf, bank.layout, len(uniq))
+        sel = torch.tensor(rng.integers(-1, len(uniq), batch), dtype=torch.int32, device="cuda")
+        gen = torch.Generator(device="cuda").manual_seed(int(rng.integers(0, 1 << 30)))
+        xs = [torch.randn(batch, s, di, device="cuda", generator=gen).bfloat16() for (_, di, _), s in zip(mods, seqs)]
+        if share:
+            xs = [xs[0]] * n_mod
+        y0 = [torch.randn(batch, s, do, device="cuda", generator=gen).bfloat16() for (_, _, do), s in zip(mods, seqs)]
+        acc, scale = bool(rng.integers(0, 2)), float(rng.choice([1.0, 0.5]))
+        desc = (n, rank, share, mods, seqs, batch, uniq, sel.tolist(), acc)
+        got = [y.clone() for y in y0]
+        offs = [bank.layout.module(nm)[3:5] for nm, _, _ in mods]
+        prepare_stacked_group(xs, got, buf, len(uniq), offs, sel, rank, scale, ws, acc)()
+        want = [y.clone() for y in y0]
+        for (nm, _, _), x, y in zip(mods, xs, want):
+            prepare_dense(x, y, st[nm][0], st[nm][1], sel, rank, scale, ws, acc)()
+        torch.cuda.synchronize()
+        for m, (g, w) in enumerate(zip(got, want)):
+            assert torch.equal(g, w), (desc, m)
+        assert _hip.workspace_errors() == 0, desc
