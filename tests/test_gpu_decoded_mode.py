@@ -152,13 +152,13 @@ def test_decode_stacked_from_int16_source_matches_packed():
         assert torch.equal(got[name][0], want[name][0]) and torch.equal(got[name][1], want[name][1])
 
 
-@pytest.mark.parametrize("accumulate", [True, False])
-def test_grouped_decoded_mode_equals_per_module_dense_calls(monkeypatch, accumulate):
+@pytest.mark.parametrize("accumulate,dtype", [(True, torch.bfloat16), (False, torch.bfloat16), (True, torch.float32)])
+def test_grouped_decoded_mode_equals_per_module_dense_calls(monkeypatch, accumulate, dtype):
     """lithe_lora_delta_grouped over dense factors in the stacked decode layout (one buffer; module
     m's A / B at n_sel * 64 * a_off / b_off): with the shrink's K split fixed, every module's output
     equals the per-module decoded-mode call over its views of the buffer bit for bit. Covers
-    modules sharing one x (one workgroup per tile and module), different widths, a 12,288-wide
-    input and an empty route."""
+    modules sharing one x (one workgroup per tile and module), different widths, an empty route,
+    and fp32 activations and factors (no grouped kernel: job by job through the per-call ones)."""
     from lithe_amd.kernels import decode_packed_stacked
     from lithe_amd.kernels.prepared import prepare_stacked_group
     monkeypatch.setenv("LITHE_SHRINK_KS", "1")
@@ -166,16 +166,16 @@ def test_grouped_decoded_mode_equals_per_module_dense_calls(monkeypatch, accumul
     _, bank = _bank(mods, 4, 90)
     uniq = [3, 0, 2]
     u = torch.tensor(uniq, dtype=torch.int32, device="cuda")
-    buf = decode_packed_stacked(bank.words, u, bank.layout, bank.pool_a, bank.pool_b)
-    st = bank.decode_stacked(uniq)
+    buf = decode_packed_stacked(bank.words, u, bank.layout, bank.pool_a, bank.pool_b, dtype=dtype)
+    st = bank.decode_stacked(uniq, dtype=dtype)
     sel = torch.tensor([2, -1, 0, 1], dtype=torch.int32, device="cuda")
     gen = torch.Generator(device="cuda").manual_seed(17)
     shape = {n: (di, do) for n, di, do in mods}
     spec = [("q", 96), ("k", 96), ("v", 96), ("up", 40), ("down", 33)]
-    xq = torch.randn(4, 96, 512, device="cuda", generator=gen).bfloat16()
-    xs = [xq if n in ("q", "k", "v") else torch.randn(4, m, shape[n][0], device="cuda", generator=gen).bfloat16()
+    xq = torch.randn(4, 96, 512, device="cuda", generator=gen).to(dtype)
+    xs = [xq if n in ("q", "k", "v") else torch.randn(4, m, shape[n][0], device="cuda", generator=gen).to(dtype)
           for n, m in spec]
-    y0 = [torch.randn(4, m, shape[n][1], device="cuda", generator=gen).bfloat16() for n, m in spec]
+    y0 = [torch.randn(4, m, shape[n][1], device="cuda", generator=gen).to(dtype) for n, m in spec]
     ws = shared_workspace("cuda", 16 << 20)
     offs = [bank.layout.module(n)[3:5] for n, _ in spec]
     got = [y.clone() for y in y0]
