@@ -210,6 +210,14 @@ def test_grouped_decoded_mode_rejects_weighted_routes():
                          shared_workspace("cuda", 1 << 20), keep=(slots, w, buf))
     with pytest.raises(ValueError):
         call()
+    # the prepared form refuses offsets that reach past the buffer, and a buffer of another dtype
+    from lithe_amd.kernels.prepared import prepare_stacked_group
+    ao, bo = bank.layout.module(name)[3:5]
+    with pytest.raises(ValueError):
+        prepare_stacked_group([x], [y], buf, 2, [(ao, bank.layout.total_blocks)], slots, 16, 1.0,
+                              shared_workspace("cuda", 1 << 20))
+    with pytest.raises(ValueError):
+        prepare_stacked_group([x], [y], buf.float(), 2, [(ao, bo)], slots, 16, 1.0, shared_workspace("cuda", 1 << 20))
 
 
 def test_random_grouped_decoded_mode_equals_per_module(monkeypatch):
