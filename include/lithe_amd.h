@@ -243,8 +243,9 @@ int32_t lithe_lora_delta_noalloc(const void *x, int32_t x_dtype, int64_t n_batch
 /* Shared-input group: n_mod modules whose linears read the same x (the to_q / to_k / to_v
  * projections of a FLUX attention block, or add_q / add_k / add_v_proj). One shrink reads x once
  * and produces the rank-r intermediate of every module (mid = x [A_0; A_1; ...]^T, stacked as
- * rank groups), then one expand per module updates y[m] (n_batch, seq, d_out[m]) exactly as
- * lithe_lora_delta would with out_scale[m] (no out_scale_vec). Factors: n_mod INDEXED entries
+ * rank groups), then the expand of every module updates y[m] (n_batch, seq, d_out[m]) exactly as
+ * lithe_lora_delta would with out_scale[m] (no out_scale_vec): one launch for all of them when
+ * the modules share one B index source and B table (bf16, packed indices), else one per module. Factors: n_mod INDEXED entries
  * that share one A index source (base, kind, levels, strides, n_slots; each module's A at its
  * own block_off) and one A value table; each module has its own B source and B table.
  * y, d_out, out_scale and factors are host arrays of n_mod entries (y[m] a device pointer).

@@ -490,6 +490,71 @@ extern "C" int32_t lithe_lora_delta_shared_x(const void *x, int32_t x_dtype, int
     hipStream_t st = (hipStream_t)stream;
     const int src = src_of(a, LITHE_FACTOR_INDEXED);
     launch_typed(true, x_dtype, y_dtype, pshrink, a, src, st);
+
+    // Expands: one grouped launch for every module when they read one B index source and one B
+    // value table (one bank; bf16, packed indices), else one launch per module. The outputs are
+    // the same either way (a module's expand sums do not depend on its tiling).
+    bool one_b = x_dtype == LITHE_DT_BF16 && y_dtype == LITHE_DT_BF16 && src == SRC_PACKED &&
+                 getenv("LITHE_GROUPED_SERIAL") == nullptr;
+    for (int m = 1; m < n_mod && one_b; ++m) {
+        const lithe_index_src &b0 = f[0].b_idx, &bm = f[m].b_idx;
+        one_b = bm.base == b0.base && bm.kind == b0.kind && bm.num_levels == b0.num_levels &&
+                bm.slot_stride == b0.slot_stride && bm.level_stride == b0.level_stride && bm.n_slots == b0.n_slots;
+        for (int l = 0; l < kMaxLevels; ++l)
+            for (int q = 0; q < 10; ++q) one_b = one_b && f[m].lut_b.value[l][q] == f[0].lut_b.value[l][q];
+    }
+    if (one_b) {
+        const PlanCtx ctx{n_batch * ((seq + 15) / 16)};
+        GroupArgs ge{};
+        ge.a = a;
+        ge.a.n_slots = std::min(f[0].a_idx.n_slots, f[0].b_idx.n_slots);
+        copy_lut(ge.a.luts.v[1], f[0].lut_b);
+        Plan pe[kMaxJobs];
+        int64_t wg = 0;
+        size_t lds_e = 0;
+        for (int m = 0; m < n_mod; ++m) {
+            const Plan p = make_plan(n_batch, seq, d_in, d_out[m], rank, routes->n_route, xbytes, false, ybytes, &ctx);
+            pe[m] = p;
+            set_shrink_fields(ge.a, p);    // G, n_rg of one module (the same for every job)
+            GroupJob &j = ge.job[m];
+            j.x = x;
+            j.y = y[m];
+            j.mid = a.mid;
+            j.seq = seq;
+            j.d_in = d_in;
+            j.d_out = d_out[m];
+            j.rows = n_batch * seq;
+            for (int g = 0; g < kMaxGroups; ++g) j.a_goff[g] = a.a_goff[g];
+            j.b_off = f[m].b_idx.block_off;
+            j.MR = ps.MR;
+            j.mid_goff = m * G1;
+            j.n_mod_wg = 1;
+            j.xnt = 1;
+            j.tiles_s = p.tiles_s;
+            j.ks = p.ks;
+            j.pb = p.pb;
+            j.arow = p.arow;
+            j.region = p.region;
+            j.red_off = p.red_off;
+            j.stage_off = p.stage_off;
+            j.tiles_e = p.tiles_e;
+            j.subs_e = p.subs_e;
+            j.BO = p.BO;
+            j.vec_y = (d_out[m] % 8 == 0) && (((uintptr_t)y[m] & 15u) == 0);
+            j.nblk_max = p.nblk_max;
+            j.estage_off = p.estage_off;
+            j.wo_sh = p.wo_sh;
+            j.out_scale = out_scale[m];
+            ge.begin[m] = (int32_t)wg;
+            const int64_t bow = (int64_t)p.BO << p.wo_sh;
+            wg += (((d_out[m] + bow - 1) / bow) * n_batch * p.tiles_e + 7) / 8 * 8;
+            lds_e = std::max(lds_e, p.lds_e);
+        }
+        ge.n_jobs = n_mod;
+        if (wg > kMaxGridX) return LITHE_ERR_SHAPE;
+        launch_expand_group_bf16_bf16(pe[0].GE, pe[0].BOM, pe[0].NS, ge, (unsigned)wg, lds_e, src, st);
+        return hipGetLastError() == hipSuccess ? LITHE_OK : LITHE_ERR_HIP;
+    }
     for (int m = 0; m < n_mod; ++m) {
         const Plan pe = make_plan(n_batch, seq, d_in, d_out[m], rank, routes->n_route, xbytes, false, ybytes);
         LoraArgs e = a;
