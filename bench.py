@@ -829,7 +829,8 @@ def main():
                    "calls_per_step": len(wl.calls)},
         "achieved_GBps": round(wl.alg_bytes / (ms * 1e-3) / 1e9, 1),
         "frac_of_peak": round(wl.alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-        "roofline": {"kernel": {"qkv": "lithe_lora_delta / lithe_lora_delta_shared_x (one shrink + one expand per module)",
+        "roofline": {"kernel": {"qkv": "lithe_lora_delta per module; lithe_lora_delta_shared_x for q / k / v (one shrink + "
+                                       "one grouped expand launch)",
                                 "grouped": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage)",
                                 "fused": "lithe_lora_delta_grouped (one shrink + one expand launch per block stage, "
                                          "q/k/v sharing x)",

@@ -104,7 +104,8 @@ def prepare_dense(x: torch.Tensor, y: torch.Tensor, a: torch.Tensor, b: torch.Te
 
 class PreparedSharedX:
     """y_m <- y_m + delta_m(x) for modules that read one input (``lithe_lora_delta_shared_x``):
-    one shrink over x for all of them, then one expand per module."""
+    one shrink over x for all of them, then their expands (one launch when the modules read one
+    B source and table, else one per module)."""
 
     def __init__(self, x: torch.Tensor, ys: Sequence[torch.Tensor], factors: Sequence[_hip.Factors],
                  route: _hip.Routes, rank: int, out_scales: Sequence[float], workspace: torch.Tensor,
